@@ -1,0 +1,193 @@
+"""Benchmark of the ragged paged-KV attention step on one MI355X.
+
+A "step" is one pass of the hot path over one batch: q/k RMSNorm + RoPE + int8 KV append of the new
+tokens, then attention (split-KV decode + gated merge). The headline workload is BASELINE.json's
+batch-8 ragged decode, contexts U[1024, 32768], int8 KV, one Qwen3.8 full-attention
+layer (24 q heads, 4 kv heads, head_dim 256), synthetic N(0,1) data. `value` is KV GB/s: algorithmic
+KV bytes of the step (every key and value of [0, ctx] read once, 2112 B per token) divided by the
+step time, with all inputs resident in HBM. The KV pool is rotated among three copies so that the
+256 MB Infinity Cache cannot serve a step from the previous one.
+
+Also reported (in "extra"): the long-context decode configs 5a/5b/5c.
+
+The CPU baseline is the reference's own ops.cpp attention (built from the reference sources into
+oracle/_ref, single-threaded, one token at a time in double precision) on the same contexts.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "qwen3.8-27b-cuda-kernel_amd")]
+
+HBM_PEAK_GBS = 8000.0
+
+
+def time_steps(run_step, steps, warmup, rotate):
+    import torch
+    for i in range(warmup):
+        run_step(i % rotate)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        run_step(i % rotate)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms
+
+
+def time_attention_only(batch, steps, rotate):
+    """Average duration of the attention launch (decode + merge kernels) alone, HIP events on the
+    launch stream, over the same rotation of pools."""
+    import torch
+    import q38a
+    s = torch.cuda.current_stream().cuda_stream
+    ap = batch.attention_params()
+    descs = [batch.kv_desc(i) for i in range(rotate)]
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        evs[i][0].record()
+        q38a.attention_decode(ap, batch.batch, descs[i % rotate], s)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / steps
+
+
+def decode_config(name, dtype, steps, warmup, pools=3):
+    import torch
+    import q38a
+    from q38a.workloads import DecodeBatch, decode_contexts
+    ctxs = decode_contexts(name)
+    batch = DecodeBatch(ctxs, dtype=dtype, seed=0, pools=pools)
+    s = torch.cuda.current_stream().cuda_stream
+    appp, ap = batch.append_params(), batch.attention_params()
+    descs = [batch.kv_desc(i) for i in range(pools)]
+
+    def step(i):
+        q38a.qk_norm_rope_append(appp, batch.batch, descs[i], s)
+        q38a.attention_decode(ap, batch.batch, descs[i], s)
+
+    ms = time_steps(step, steps, warmup, pools)
+    attn_ms = time_attention_only(batch, steps, pools)
+    kv = batch.kv_bytes()
+    return {
+        "config": name, "ctxs": ctxs, "kv_dtype": "int8" if dtype == q38a.KV_INT8 else "bf16",
+        "ms_per_step": ms, "tokens_per_s": batch.B / (ms * 1e-3),
+        "kv_bytes": kv, "kv_gbs": kv / (ms * 1e-3) / 1e9,
+        "attn_ms": attn_ms, "attn_gbs": (kv + batch.io_bytes()) / (attn_ms * 1e-3) / 1e9,
+        "_batch": batch,
+    }
+
+
+def cpu_baseline(batch, budget_s=20.0):
+    """Reference CPU attention (oracle/_ref: src/ref/ops.cpp attention_token) on the GPU batch's own
+    pages, single-threaded. Sequences are timed one after another until the budget is spent."""
+    import numpy as np
+    import q38a
+    from oracle.oracle import REF_LIB, Oracle, Reference
+    kind = "reference" if os.path.exists(REF_LIB) else "port"
+    orc = Oracle()
+    pool = batch.pools[0].cpu().numpy()
+    q16 = batch.q16.cpu().numpy().view(np.uint16).reshape(batch.B, 24, 256)
+    gate = batch.proj.cpu().view(__import__("torch").int16).numpy().view(np.uint16)[:, 24 * 256:48 * 256]
+
+    def f16_to_f32(h):
+        return np.asarray(h, np.uint16).view(np.float16).astype(np.float32)
+
+    def bf16_to_f32(b):
+        return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+    ref = Reference() if kind == "reference" else None
+    done_tokens, done_bytes, spent = 0, 0, 0.0
+    order = sorted(range(batch.B), key=lambda b: batch.ctxs[b])
+    for b in order:
+        L = batch.ctxs[b] + 1
+        k, v = orc.read_back(pool, batch.dtype, 4, batch.block_table, b, L)
+        q = f16_to_f32(q16[b]).ravel()
+        g = bf16_to_f32(gate[b])
+        if kind == "reference":
+            st = ref.store(4, L)
+            st.k[...] = k
+            st.v[...] = v
+            t0 = time.perf_counter()
+            st.attention_token(24, q, g, L - 1)
+            dt = time.perf_counter() - t0
+            st.close()
+        else:
+            t0 = time.perf_counter()
+            orc.attention_token(q, g, L - 1, k, v, 24, 4)
+            dt = time.perf_counter() - t0
+        spent += dt
+        done_tokens += 1
+        done_bytes += L * (2112 if batch.dtype == q38a.KV_INT8 else 4096)
+        if spent > budget_s:
+            break
+    return {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{done_tokens} of {batch.B} decode rows (shortest first), one attention layer, "
+                      f"{done_bytes / 2112 if batch.dtype == 0 else done_bytes / 4096:.0f} KV tokens, "
+                      f"{spent:.2f} s single-threaded; tokens/s = {done_tokens / spent:.3f}",
+            "tokens_per_s": done_tokens / spent}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of configs to run (default: all)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the single-GPU number is the reported value.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import q38a
+    torch.cuda.init()
+    only = set(filter(None, args.only.split(",")))
+    extra = {}
+    head = decode_config("decode_b8", q38a.KV_INT8, args.steps, args.warmup)
+    for name, dt in (("long_b8", q38a.KV_INT8), ("long_b1", q38a.KV_INT8), ("long_b8_bf16", q38a.KV_BF16)):
+        if only and name not in only:
+            continue
+        r = decode_config(name, dt, args.steps, args.warmup)
+        r.pop("_batch")
+        r["hbm_frac"] = r["attn_gbs"] / HBM_PEAK_GBS
+        extra[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items() if k != "ctxs"}
+        extra[name]["sum_ctx"] = sum(r["ctxs"])
+    batch = head.pop("_batch")
+    cpu = None if args.no_cpu else cpu_baseline(batch)
+    line = {
+        "metric": "decode-attn KV GB/s (% HBM peak) + mixed-batch step tokens/s, batch 8",
+        "value": round(head["kv_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: N(0,1) bf16 q/k/v/gate, prior KV quantized with the reference int8 quantizer, "
+                "random page permutation",
+        "config": {"workload": "configs[1] batched decode: 8 seqs x 1 token, ctx U[1024,32768] seed 0, "
+                               "24q/4kv heads, head_dim 256, int8 64-token pages",
+                   "sum_ctx": sum(head["ctxs"]), "tokens_per_step": 8},
+        "roofline": {"bound": "hbm", "achieved": round(head["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attention_decode (attn_decode_kernel + attn_merge_kernel)",
+                     "kernel_ms": round(head["attn_ms"], 5)},
+        "cpu_baseline": cpu,
+        "tokens_per_s": round(head["tokens_per_s"], 1),
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,208 @@
+// Fused q/k offset-RMSNorm + partial RoPE + KV append for gfx950.
+//
+// Behaviour follows the reference kernel src/kernels/qk_norm_rope.cu:12-90 and, to the last bit,
+// its CPU twin src/ref/ops.cpp:79-142:
+//   y = x * r * w with r = 1 / sqrt(float(sum_sq / 256) + eps), sum_sq accumulated in double;
+//   RoPE on dims [0, 64): (y_i, y_{i+32}) <- (y_i c - y_{i+32} s, y_{i+32} c + y_i s);
+//   q -> fp16 (RNE); k (normed + rotated) and v (as projected) -> page row: int8 with one fp16
+//   scale = fp16(amax / 127) per 64-dim group and codes clamp(rint(y / scale), -127, 127), or bf16.
+//
+// Work mapping (MI355X-first): one wave64 per (token, head row); rows are the nq q heads, then the
+// nkv k heads, then the nkv v heads of a token. Lane l owns dims [4l, 4l + 4), so a 64-dim
+// quantisation group is exactly 16 lanes (one DPP row) and RoPE partners (i, i + 32) sit 8 lanes
+// apart. Contraction is off for the whole file and division / square root go through binary64, so
+// every operation rounds exactly as the reference's IEEE single-precision code does. cos/sin come
+// from a host-built table (same libm calls as the CPU reference), read per position.
+//
+// Sum of squares: the reference sums x_i^2 in double, left to right. x is bf16, so every x_i^2 is
+// exact in double; the sum is exact in any order whenever the nonzero magnitudes span at most 14
+// binades (24 + 2 * 14 <= 53 bits). The kernel checks that span (wave-wide min/max exponent) and
+// then uses a tree reduction; otherwise one lane replays the left-to-right double sum from LDS.
+#include "common.hpp"
+
+// No multiply-add fusion anywhere in this file: every product and sum rounds on its own, as in the
+// reference's x86-64 build.
+#pragma clang fp contract(off)
+
+namespace q38a {
+namespace {
+
+// Correctly rounded binary32 division and square root, computed in binary64 and rounded once:
+// for these operations a 53-bit intermediate (>= 2 * 24 + 2 bits) makes the double rounding
+// innocuous, so the result equals the IEEE single-precision operation whatever fast-math
+// defaults the device library applies to float sqrt/div.
+__device__ inline float div_rn(float a, float b) { return float(double(a) / double(b)); }
+__device__ inline float sqrt_rn(float a) { return float(__builtin_sqrt(double(a))); }
+
+constexpr int kWavesPerBlock = 4;
+
+__device__ inline int exponent_of(float x) {  // floor(log2|x|) for normal x; -149 for subnormals
+  const uint32_t e = (as_u32(x) >> 23) & 0xffu;
+  return e == 0 ? -149 : int(e) - 127;
+}
+
+__device__ inline double wave_sum(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+struct AppendArgs {
+  const uint16_t* proj;
+  int ld_proj;
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  int nq, nkv;
+  uint16_t* q_out;
+  int attn_layer;
+  const float* rope;  // [rope_rows][64]
+  int rope_rows;
+};
+
+__global__ void __launch_bounds__(kWavesPerBlock * 64)
+qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
+  __shared__ float stage[kWavesPerBlock][kHeadDim];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int job = blockIdx.x * kWavesPerBlock + wave;
+  if (job >= jobs) return;
+  const int rows = p.nq + 2 * p.nkv;
+  const int m = job / rows, r = job % rows;
+  const bool is_q = r < p.nq, is_k = !is_q && r < p.nq + p.nkv;
+  // q head r at column r*256; k head h at (2nq + h)*256; v head h at (2nq + nkv + h)*256
+  const int col = (is_q ? r : p.nq + r) * kHeadDim;
+  const int pos = batch.tok_pos[m];
+
+  const uint2 raw = *reinterpret_cast<const uint2*>(p.proj + size_t(m) * p.ld_proj + col + 4 * lane);
+  float x[4] = {bf16_value(uint16_t(raw.x)), bf16_value(uint16_t(raw.x >> 16)), bf16_value(uint16_t(raw.y)),
+                bf16_value(uint16_t(raw.y >> 16))};
+  const bool pos_ok = pos >= 0 && pos < p.rope_rows;
+
+  if (is_q || is_k) {
+    // ---- sum of squares, bit-identical to the left-to-right double sum --------------------------
+    int emin = 1 << 20, emax = -(1 << 20);
+    double part = 0.0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      part += double(x[e]) * double(x[e]);
+      if (x[e] != 0.0f) {
+        const int ex = exponent_of(x[e]);
+        emin = min(emin, ex);
+        emax = max(emax, ex);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      emin = min(emin, __shfl_xor(emin, off, 64));
+      emax = max(emax, __shfl_xor(emax, off, 64));
+    }
+    double ss;
+    if (emax - emin <= 14) {
+      ss = wave_sum(part);  // exact in any order
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) stage[wave][4 * lane + e] = x[e];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      double seq = 0.0;
+      if (lane == 0) {
+        for (int i = 0; i < kHeadDim; ++i) {
+          const double v = double(stage[wave][i]);
+          seq = seq + v * v;
+        }
+      }
+      ss = __shfl(seq, 0, 64);
+    }
+    const float mean = float(ss / double(kHeadDim));
+    const float rs = div_rn(1.0f, sqrt_rn(mean + p.eps));
+    const float* w = is_q ? p.q_norm : p.k_norm;
+    const float4 wv = *reinterpret_cast<const float4*>(w + 4 * lane);
+    const float wl[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = (x[e] * rs) * wl[e];
+
+    // ---- partial RoPE: lanes 0-7 own dims 0-31, lanes 8-15 own dims 32-63 -----------------------
+    float partner[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) partner[e] = __shfl_xor(x[e], 8, 64);
+    if (lane < 16 && pos_ok) {
+      const int i0 = 4 * (lane & 7);
+      const float* cs = p.rope + size_t(pos) * kRotaryDim;
+      const float4 c4 = *reinterpret_cast<const float4*>(cs + i0);
+      const float4 s4 = *reinterpret_cast<const float4*>(cs + 32 + i0);
+      const float c[4] = {c4.x, c4.y, c4.z, c4.w}, s[4] = {s4.x, s4.y, s4.z, s4.w};
+      if (lane < 8) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = x[e] * c[e] - partner[e] * s[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = x[e] * c[e] + partner[e] * s[e];
+      }
+    }
+  }
+
+  if (is_q) {
+    uint16_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = pos_ok ? f16_bits(x[e]) : uint16_t(0x7e00u);  // NaN flags a bad position
+    uint2 out;
+    out.x = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
+    out.y = uint32_t(h[2]) | (uint32_t(h[3]) << 16);
+    *reinterpret_cast<uint2*>(p.q_out + (size_t(m) * p.nq + r) * kHeadDim + 4 * lane) = out;
+    return;
+  }
+
+  const int head = is_k ? r - p.nq : r - p.nq - p.nkv;
+  const int slot = batch.seq_slot[batch.tok_seq[m]];
+  const int page_idx = pos / kPageTokens;
+  if (!pos_ok || page_idx >= kv.max_pages_per_seq) return;
+  const int page = kv.block_table[size_t(slot) * kv.max_pages_per_seq + page_idx];
+  const int tok = pos % kPageTokens;
+  uint8_t* base = kv.pool + size_t(p.attn_layer) * kv.layer_stride + size_t(page) * kv.page_bytes;
+  const size_t row = is_k ? kv.layout.k_row(head, tok) : kv.layout.v_row(head, tok);
+
+  if (kv.layout.dtype == Q38A_KV_BF16) {
+    uint2 out;
+    out.x = uint32_t(bf16_bits(x[0])) | (uint32_t(bf16_bits(x[1])) << 16);
+    out.y = uint32_t(bf16_bits(x[2])) | (uint32_t(bf16_bits(x[3])) << 16);
+    *reinterpret_cast<uint2*>(base + row + 8 * lane) = out;
+    return;
+  }
+
+  // int8: group g = lane / 16 covers dims [64g, 64g + 64)
+  float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  const uint16_t sbits = f16_bits(div_rn(amax, 127.0f));
+  const float scale = f16_value(sbits);
+  uint32_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float q = 0.0f;
+    if (scale > 0.0f) q = fminf(fmaxf(__builtin_rintf(div_rn(x[e], scale)), -127.0f), 127.0f);
+    packed |= (uint32_t(int32_t(q)) & 0xffu) << (8 * e);
+  }
+  *reinterpret_cast<uint32_t*>(base + row + 4 * lane) = packed;
+  if ((lane & 15) == 0) {
+    const size_t so = is_k ? kv.layout.k_scales(head, tok) : kv.layout.v_scales(head, tok);
+    reinterpret_cast<uint16_t*>(base + so)[lane >> 4] = sbits;
+  }
+}
+
+}  // namespace
+
+int launch_qk_norm_rope_append(const q38a_qk_norm_rope_params& p, const q38a_batch_desc& b,
+                               const q38a_kv_cache_desc& kv, hipStream_t stream) {
+  if (b.num_tokens == 0) return Q38A_OK;
+  const int rows = p.num_q_heads + 2 * p.num_kv_heads;
+  const long long jobs = (long long)b.num_tokens * rows;
+  if (jobs > (1ll << 30)) return set_error(Q38A_ERR_INVALID, "qk_norm_rope_append: too many tokens (%d)", b.num_tokens);
+  AppendArgs a{p.proj, p.ld_proj, p.q_norm, p.k_norm, p.eps, p.num_q_heads, p.num_kv_heads, p.q_out,
+               p.attn_layer, p.rope_cos_sin, p.rope_rows};
+  const int blocks = int((jobs + kWavesPerBlock - 1) / kWavesPerBlock);
+  hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(blocks), dim3(kWavesPerBlock * 64), 0, stream, a,
+                     to_args(b), to_args(kv), int(jobs));
+  return check_hip(hipGetLastError(), "qk_norm_rope_append launch");
+}
+
+}  // namespace q38a

@@ -1,0 +1,135 @@
+// Shared host/device definitions of the q38a library: error reporting, the paged KV byte layout,
+// exact 16-bit float conversions and the MFMA operand vector types used by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "q38a.h"
+
+namespace q38a {
+
+constexpr int kPageTokens = Q38A_PAGE_TOKENS;
+constexpr int kHeadDim = Q38A_HEAD_DIM;
+constexpr int kRotaryDim = 64;  // partial RoPE over dims [0, 64): pairs (i, i + 32)
+
+// ---- errors (host) ------------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);  // records the message, returns `code`
+void clear_error();
+int check_hip(hipError_t e, const char* what);   // Q38A_OK or Q38A_ERR_HIP with the HIP message
+int device_cu_count(int* out);                   // cached per device
+
+// ---- paged KV layout (reference kernels.h:41-70, docs/FORMAT.md 3.1) --------------------------
+// One (layer, page) block, int8:  K [kvh][64][256] i8 | V [kvh][64][256] i8 |
+//                                 K scales [kvh][64][4] f16 | V scales [kvh][64][4] f16
+//                         bf16:   K [kvh][64][256] bf16 | V [kvh][64][256] bf16
+struct PageLayout {
+  int kv_heads;
+  int dtype;
+  __host__ __device__ size_t elem() const { return dtype == Q38A_KV_INT8 ? 1 : 2; }
+  __host__ __device__ size_t k_row(int h, int t) const {
+    return (size_t(h) * kPageTokens + t) * kHeadDim * elem();
+  }
+  __host__ __device__ size_t v_row(int h, int t) const {
+    return size_t(kv_heads) * kPageTokens * kHeadDim * elem() + k_row(h, t);
+  }
+  __host__ __device__ size_t k_scales(int h, int t) const {
+    return 2 * size_t(kv_heads) * kPageTokens * kHeadDim + (size_t(h) * kPageTokens + t) * 8;
+  }
+  __host__ __device__ size_t v_scales(int h, int t) const {
+    return k_scales(h, t) + size_t(kv_heads) * kPageTokens * 8;
+  }
+  __host__ __device__ size_t page_bytes() const {
+    return dtype == Q38A_KV_INT8 ? 2 * size_t(kv_heads) * kPageTokens * (kHeadDim + 8)
+                                 : 2 * size_t(kv_heads) * kPageTokens * kHeadDim * 2;
+  }
+};
+
+// ---- exact conversions --------------------------------------------------------------------------
+__host__ __device__ inline uint32_t as_u32(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  return u;
+}
+__host__ __device__ inline float as_f32(uint32_t u) {
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+// IEEE binary16 from binary32, round to nearest even; NaN -> quiet NaN, overflow -> inf.
+__device__ inline uint16_t f16_bits(float f) {
+  const uint32_t u = as_u32(f);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t mag = u & 0x7fffffffu;
+  if (mag > 0x7f800000u) return uint16_t(sign | 0x7e00u);
+  if (mag >= 0x477ff000u) return uint16_t(sign | 0x7c00u);  // |f| >= 65520 rounds to inf
+  if (mag < 0x38800000u) {  // below 2^-14: result is a multiple of 2^-24
+    return uint16_t(sign | uint32_t(__builtin_rintf(as_f32(mag) * 16777216.0f)));
+  }
+  // normal: drop 13 mantissa bits with round-half-even, rebias the exponent 127 -> 15
+  const uint32_t rounded = (mag + 0x0fffu + ((mag >> 13) & 1u)) >> 13;
+  return uint16_t(sign | (rounded - (112u << 10)));
+}
+
+__device__ inline float f16_value(uint16_t h) {
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  float v;
+  if (e == 0) v = float(m) * 5.9604644775390625e-08f;  // m * 2^-24, exact
+  else if (e == 31) v = as_f32(0x7f800000u | (m << 13));
+  else v = as_f32(((e + 112u) << 23) | (m << 13));
+  return (h & 0x8000u) ? -v : v;
+}
+
+// bfloat16 from binary32, round to nearest even; NaN -> quiet NaN.
+__host__ __device__ inline uint16_t bf16_bits(float f) {
+  const uint32_t u = as_u32(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  return uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__host__ __device__ inline float bf16_value(uint16_t b) { return as_f32(uint32_t(b) << 16); }
+
+// ---- MFMA operand types (gfx950) ----------------------------------------------------------------
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+// Kernel-side copies of the C descriptors (passed by value as kernel arguments).
+struct BatchArgs {
+  int num_seqs, num_tokens, max_tokens_per_seq;
+  const int32_t* seq_start;
+  const int32_t* seq_slot;
+  const int32_t* seq_pos0;
+  const int32_t* tok_pos;
+  const int32_t* tok_seq;
+};
+struct KvArgs {
+  uint8_t* pool;
+  PageLayout layout;
+  int num_pages;
+  size_t page_bytes;
+  size_t layer_stride;
+  const int32_t* block_table;
+  int max_pages_per_seq;
+};
+
+inline BatchArgs to_args(const q38a_batch_desc& b) {
+  return BatchArgs{b.num_seqs, b.num_tokens, b.max_tokens_per_seq, b.seq_start,
+                   b.seq_slot, b.seq_pos0,   b.tok_pos,            b.tok_seq};
+}
+inline KvArgs to_args(const q38a_kv_cache_desc& k) {
+  return KvArgs{k.pool, PageLayout{k.kv_heads, k.dtype}, k.num_pages, k.page_bytes, k.layer_stride,
+                k.block_table, k.max_pages_per_seq};
+}
+
+// Host-side validation shared by the launchers.
+int validate_batch(const q38a_batch_desc* b, bool need_tok);
+int validate_kv(const q38a_kv_cache_desc* k);
+
+}  // namespace q38a
