@@ -187,8 +187,9 @@ int q38a_attention_decode_splits(int batch_seqs, int kv_heads, int num_sms, int 
   (void)batch_seqs;
   (void)kv_heads;
   (void)num_sms;
-  // Splits are chosen per sequence on the device (balanced by pages); max_splits bounds them.
-  return max_splits < 1 ? 1 : max_splits;
+  // Splits are chosen per sequence on the device (balanced by pages); max_splits bounds them and
+  // the launchers accept at most 512.
+  return max_splits < 1 ? 1 : (max_splits > 512 ? 512 : max_splits);
 }
 
 size_t q38a_split_scratch_floats(int rows, int num_q_heads, int max_splits) {

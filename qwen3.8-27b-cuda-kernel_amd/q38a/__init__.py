@@ -20,7 +20,7 @@ KV_INT8 = 0
 KV_BF16 = 1
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libq38a.so")
+LIB_PATH = os.environ.get("Q38A_LIB") or os.path.join(os.path.dirname(_HERE), "lib", "libq38a.so")
 
 
 class Q38AError(RuntimeError):
