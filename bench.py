@@ -23,6 +23,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "qwen3.8-27b-cuda-kernel_amd")]
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
 
 
 def time_steps(run_step, steps, warmup, rotate):
@@ -80,6 +81,33 @@ def decode_config(name, dtype, steps, warmup, pools=3):
         "attn_ms": attn_ms, "attn_gbs": (kv + batch.io_bytes()) / (attn_ms * 1e-3) / 1e9,
         "_batch": batch,
     }
+
+
+def prefill_config(steps, warmup):
+    """Config 3: one sequence appends a 2048-token chunk onto a 6000-token int8 prefix."""
+    import torch
+    import q38a
+    from q38a.workloads import RaggedBatch
+    rb = RaggedBatch([(6000, 2048)], seed=0)
+    s = torch.cuda.current_stream().cuda_stream
+    appp, ap, kvd = rb.append_params(), rb.attention_params(), rb.kv_desc(0)
+
+    def step(i):
+        q38a.qk_norm_rope_append(appp, rb.batch, kvd, s)
+        q38a.attention_prefill(ap, rb.batch, kvd, s)
+
+    ms = time_steps(step, steps, warmup, 1)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        evs[i][0].record()
+        q38a.attention_prefill(ap, rb.batch, kvd, s)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    attn_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
+    fl = rb.flops()
+    return {"config": "prefill_2048_on_6000", "ms_per_step": round(ms, 5), "tokens_per_s": round(2048 / (ms * 1e-3), 1),
+            "attn_ms": round(attn_ms, 5), "flops": fl, "attn_tflops": round(fl / (attn_ms * 1e-3) / 1e12, 2),
+            "mfma_frac": round(fl / (attn_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
 
 
 def cpu_baseline(batch, budget_s=20.0):
@@ -159,6 +187,8 @@ def main():
         r["hbm_frac"] = r["attn_gbs"] / HBM_PEAK_GBS
         extra[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items() if k != "ctxs"}
         extra[name]["sum_ctx"] = sum(r["ctxs"])
+    if not only or "prefill" in only:
+        extra["prefill_2048_on_6000"] = prefill_config(max(10, args.steps // 5), 3)
     batch = head.pop("_batch")
     cpu = None if args.no_cpu else cpu_baseline(batch)
     line = {

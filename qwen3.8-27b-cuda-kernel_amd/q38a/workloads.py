@@ -115,3 +115,65 @@ class DecodeBatch:
     def io_bytes(self):
         """q (fp16) + gate (bf16) reads and the bf16 output write per step."""
         return self.B * NQ * HD * 2 * 3
+
+
+def prefill_flops(seqs):
+    """Unmasked causal (query, key) pairs x 4 * head_dim * nq: 2 flops per multiply-add of QK^T
+    and of PV. seqs: [(prefix, n)]."""
+    pairs = sum(n * prefix + n * (n + 1) // 2 for prefix, n in seqs)
+    return 4 * HD * NQ * pairs
+
+
+class RaggedBatch:
+    """A continuous-batching step: sequences [(prefix, n)] (n == 1: decode row, n > 1: prefill
+    chunk), pages of all sequences interleaved by one random permutation of the pool."""
+
+    def __init__(self, seqs, dtype=q38a.KV_INT8, seed=0, pools=1):
+        self.seqs = list(seqs)
+        self.B = len(seqs)
+        self.dtype = dtype
+        rng = np.random.default_rng(seed + 1)
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        pages = [(p + n + 63) // 64 for p, n in self.seqs]
+        self.num_pages = sum(pages)
+        perm = rng.permutation(self.num_pages).astype(np.int32)
+        self.max_pages = max(pages)
+        bt = np.zeros((self.B, self.max_pages), np.int32)
+        o = 0
+        for b, pg in enumerate(pages):
+            bt[b, :pg] = perm[o:o + pg]
+            o += pg
+        self.block_table = bt
+        self.bt_t = torch.from_numpy(bt).cuda()
+        self.pools = [random_pool(self.num_pages, dtype, gen) for _ in range(pools)]
+        self.page_bytes = q38a.page_bytes(dtype, NKV)
+        seq_start = np.zeros(self.B + 1, np.int32)
+        tok_pos, tok_seq = [], []
+        for b, (p, n) in enumerate(self.seqs):
+            seq_start[b + 1] = seq_start[b] + n
+            tok_pos += list(range(p, p + n))
+            tok_seq += [b] * n
+        self.M = int(seq_start[-1])
+        self.meta = [torch.from_numpy(np.asarray(a, np.int32)).cuda() for a in (
+            seq_start, np.arange(self.B), [p for p, _ in self.seqs], tok_pos, tok_seq)]
+        self.batch = q38a.BatchDesc(self.B, self.M, max(n for _, n in self.seqs), *[t.data_ptr() for t in self.meta])
+        self.proj = torch.randn((self.M, LD), generator=gen, device="cuda").to(torch.bfloat16)
+        self.q_norm = (1.0 + 0.1 * torch.randn(HD, generator=gen, device="cuda")).float()
+        self.k_norm = (1.0 + 0.1 * torch.randn(HD, generator=gen, device="cuda")).float()
+        self.rope = torch.from_numpy(q38a.rope_table(0, max(p + n for p, n in self.seqs))).cuda()
+        self.q16 = torch.empty((self.M, NQ * HD), dtype=torch.float16, device="cuda")
+        self.out = torch.empty((self.M, NQ * HD), dtype=torch.bfloat16, device="cuda")
+        self.max_splits = 256
+        self.scratch = torch.empty(q38a.split_scratch_floats(self.B, NQ, self.max_splits), dtype=torch.float32,
+                                   device="cuda")
+
+    kv_desc = DecodeBatch.kv_desc
+    append_params = DecodeBatch.append_params
+    attention_params = DecodeBatch.attention_params
+
+    def flops(self):
+        return prefill_flops([(p, n) for p, n in self.seqs if n > 1])
+
+    def decode_kv_bytes(self):
+        per = INT8_TOKEN_BYTES if self.dtype == q38a.KV_INT8 else BF16_TOKEN_BYTES
+        return sum(p + 1 for p, n in self.seqs if n == 1) * per
