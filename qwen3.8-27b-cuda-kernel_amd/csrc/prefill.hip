@@ -34,6 +34,7 @@ constexpr int kKStride = kHeadDim + 8;    // halves per K row in LDS (16 B pad: 
 constexpr int kVStride = kKeyTile + 4;    // halves per V^T row in LDS (8 B pad)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kScoreScale = kLog2e / 16.0f;
+constexpr float kRescaleSlack = 8.0f;
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -65,19 +66,30 @@ struct RawTile {
 
 __device__ inline uint16_t half_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 
-__device__ inline void load_raw(RawTile& R, const uint8_t* pg, const PageLayout& L, int kvh, int key0, int tid) {
-  {
-    const int key = key0 + (tid >> 3), d0 = 32 * (tid & 7);
-    const uint8_t* row = pg + L.k_row(kvh, key);
-    R.k[0] = *reinterpret_cast<const u32x4*>(row + d0);
-    R.k[1] = *reinterpret_cast<const u32x4*>(row + d0 + 16);
-    R.ks = *reinterpret_cast<const uint16_t*>(pg + L.k_scales(kvh, key) + 2 * ((tid & 7) >> 1));
-  }
-  const int kb = key0 + 8 * (tid >> 6), d0 = 4 * (tid & 63), g = (tid & 63) >> 4;
+// Per-lane byte offsets of a thread's share of a tile, relative to the tile's first key row (K
+// and V rows) or first scale entry; V rows and V scales of the 8 keys follow at +256 / +8 per key.
+struct TileOffsets {
+  int k, ks, v, vs;
+};
+
+__device__ inline TileOffsets tile_offsets(const PageLayout& L, int kvh, int tid) {
+  TileOffsets o;
+  o.k = int(L.k_row(kvh, tid >> 3)) + 32 * (tid & 7);
+  o.ks = int(L.k_scales(kvh, tid >> 3)) + 2 * ((tid & 7) >> 1);
+  o.v = int(L.v_row(kvh, 8 * (tid >> 6))) + 4 * (tid & 63);
+  o.vs = int(L.v_scales(kvh, 8 * (tid >> 6))) + 2 * ((tid & 63) >> 4);
+  return o;
+}
+
+// rows: page + 256 * (first key of the tile within the page); sc: page + 8 * (same key)
+__device__ inline void load_raw(RawTile& R, const uint8_t* rows, const uint8_t* sc, const TileOffsets& o) {
+  R.k[0] = *reinterpret_cast<const u32x4*>(rows + o.k);
+  R.k[1] = *reinterpret_cast<const u32x4*>(rows + o.k + 16);
+  R.ks = *reinterpret_cast<const uint16_t*>(sc + o.ks);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    R.v[e] = *reinterpret_cast<const uint32_t*>(pg + L.v_row(kvh, kb + e) + d0);
-    R.vs[e] = *reinterpret_cast<const uint16_t*>(pg + L.v_scales(kvh, kb + e) + 2 * g);
+    R.v[e] = *reinterpret_cast<const uint32_t*>(rows + o.v + kHeadDim * e);
+    R.vs[e] = *reinterpret_cast<const uint16_t*>(sc + o.vs + 8 * e);
   }
 }
 
@@ -130,7 +142,7 @@ __device__ inline void store_tile(KvTile& T, const RawTile& R, int key0, int lim
   }
 }
 
-__global__ void __launch_bounds__(kPThreads, 1) attn_prefill_kernel(PrefillArgs a, BatchArgs batch, KvArgs kv) {
+__global__ void __launch_bounds__(kPThreads, 2) attn_prefill_kernel(PrefillArgs a, BatchArgs batch, KvArgs kv) {
   __shared__ KvTile tiles[2];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -173,17 +185,19 @@ __global__ void __launch_bounds__(kPThreads, 1) attn_prefill_kernel(PrefillArgs 
   for (int dt = 0; dt < 8; ++dt) O[dt] = float16_t{};
   float m_run = -INFINITY, l_run = 0.f;
 
+  // The next tile's raw bytes are loaded into registers while the current tile is computed from
+  // LDS, then dequantised into the other LDS buffer.
   RawTile R;
   auto page_ptr = [&](int key0) { return layer + size_t(bt[key0 / kPageTokens]) * kv.page_bytes; };
-  load_raw(R, page_ptr(0), kv.layout, kvh, 0, tid);
-  store_tile(tiles[0], R, 0, kend, tid);
-  __syncthreads();
-
-  for (int j = 0; j < ntiles; ++j) {
-    const int key0 = j * kKeyTile;
-    const bool more = j + 1 < ntiles;
-    if (more) load_raw(R, page_ptr(key0 + kKeyTile), kv.layout, kvh, (key0 + kKeyTile) % kPageTokens, tid);
-    const KvTile& T = tiles[j & 1];
+  const TileOffsets toff = tile_offsets(kv.layout, kvh, tid);
+  auto fetch = [&](RawTile& RT, int j) {
+    if (j < ntiles) {  // uniform
+      const uint8_t* pg = page_ptr(j * kKeyTile);
+      const int in_page = (j * kKeyTile) % kPageTokens;
+      load_raw(RT, pg + in_page * kHeadDim, pg + in_page * 8, toff);
+    }
+  };
+  auto compute = [&](const KvTile& T, int key0) {
 
     // S^T = K . Q^T: element 4 blk + r is key key0 + 8 blk + 4 kg + r of this lane's row
     float16_t S = {};
@@ -191,6 +205,8 @@ __global__ void __launch_bounds__(kPThreads, 1) attn_prefill_kernel(PrefillArgs 
     for (int s = 0; s < 16; ++s) {
       const half8_t kf = *reinterpret_cast<const half8_t*>(&T.k[col][16 * s + 8 * kg]);
       S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], S, 0, 0, 0);
+      // bound how far the scheduler hoists operand reads (keeps the live register set small)
+      if ((s & 3) == 3) __builtin_amdgcn_sched_barrier(0);
     }
     const bool need_mask = key0 + kKeyTile - 1 > wave_qpos_min;  // wave-uniform
     float tmax = -INFINITY;
@@ -205,24 +221,29 @@ __global__ void __launch_bounds__(kPThreads, 1) attn_prefill_kernel(PrefillArgs 
       tmax = fmaxf(tmax, x);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mnew = fmaxf(m_run, tmax);
-    // rows with no visible key yet keep m = -inf; use 0 as the exponent base for them
-    const float base = mnew == -INFINITY ? 0.f : mnew;
-    const float corr = exp2f(m_run - base);
+    // Lazy rescaling: the running reference max only moves when a tile's max exceeds it by more
+    // than kRescaleSlack (log2 units), so probabilities stay below 2^kRescaleSlack (exact enough in
+    // fp16 and fp32) and the O rescale is almost never needed after the first tiles.
+    const bool bump = tmax > m_run + kRescaleSlack;
+    float corr = 1.0f;
+    if (__any(bump)) {
+      const float mnew = bump ? tmax : m_run;
+      corr = bump ? __builtin_amdgcn_exp2f(m_run - mnew) : 1.0f;
+      m_run = mnew;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) O[dt] *= corr;
+    }
+    // a row that has seen no key yet keeps m = -inf; 0 is then a safe exponent base
+    const float base = m_run == -INFINITY ? 0.f : m_run;
     float psum = 0.f;
     half4_t P[4];  // P^T of this lane: keys 8 blk + 4 kg + r -> P[blk][r]
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float pe = exp2f(S[e] - base);
+      const float pe = __builtin_amdgcn_exp2f(S[e] - base);
       psum += pe;
       P[e >> 2][e & 3] = _Float16(pe);
     }
     l_run = l_run * corr + psum;
-    m_run = mnew;
-    if (__any(corr != 1.0f)) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) O[dt] *= corr;
-    }
     // O^T += V^T . P^T: MFMA step t covers keys 16 t + {0..3, 8..11} (k-group 0) and
     // 16 t + {4..7, 12..15} (k-group 1), matching where P^T already sits
 #pragma unroll
@@ -237,9 +258,19 @@ __global__ void __launch_bounds__(kPThreads, 1) attn_prefill_kernel(PrefillArgs 
         const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + kk + 8);
         const half8_t va = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
         O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, O[dt], 0, 0, 0);
+        if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (more) store_tile(tiles[(j + 1) & 1], R, key0 + kKeyTile, kend, tid);
+  };
+  fetch(R, 0);
+  store_tile(tiles[0], R, 0, kend, tid);
+  __syncthreads();
+  for (int j = 0; j < ntiles; ++j) {
+    fetch(R, j + 1);
+    compute(tiles[j & 1], j * kKeyTile);
+    // unconditional (past the last tile it only fills the idle buffer) so that the dequantisation
+    // can be scheduled between the MFMAs of this tile
+    store_tile(tiles[(j + 1) & 1], R, (j + 1) * kKeyTile, kend, tid);
     __syncthreads();
   }
 
