@@ -8,7 +8,9 @@ KV bytes of the step (every key and value of [0, ctx] read once, 2112 B per toke
 step time, with all inputs resident in HBM. The KV pool is rotated among three copies so that the
 256 MB Infinity Cache cannot serve a step from the previous one.
 
-Also reported (in "extra"): the long-context decode configs 5a/5b/5c.
+Also reported (in "extra"): the long-context decode configs 5a/5b/5c, the chunked prefill of
+config 3 (separate prefill launch and through the ragged launch) and the mixed continuous-batching
+step of config 4 (one 512-token chunk + 7 decode rows in one ragged launch; tokens/s = 519 / step).
 
 The CPU baseline is the reference's own ops.cpp attention (built from the reference sources into
 oracle/_ref, single-threaded, one token at a time in double precision) on the same contexts.
@@ -110,6 +112,38 @@ def prefill_config(steps, warmup):
             "mfma_frac": round(fl / (attn_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
 
 
+def ragged_config(name, seqs, steps, warmup, pools=3):
+    """One continuous-batching step through the single ragged launch (q38a_attention_ragged):
+    append of every new token, then decode rows and prefill chunks together. Config 4 is one
+    512-token chunk + 7 decode rows; t_roof = decode KV bytes / HBM peak + prefill flops / MFMA peak."""
+    import torch
+    import q38a
+    from q38a.workloads import RaggedBatch
+    rb = RaggedBatch(seqs, seed=0, pools=pools)
+    s = torch.cuda.current_stream().cuda_stream
+    appp, ap = rb.append_params(), rb.attention_params()
+    descs = [rb.kv_desc(i) for i in range(pools)]
+
+    def step(i):
+        q38a.qk_norm_rope_append(appp, rb.batch, descs[i], s)
+        q38a.attention_ragged(ap, rb.batch, descs[i], s)
+
+    ms = time_steps(step, steps, warmup, pools)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        evs[i][0].record()
+        q38a.attention_ragged(ap, rb.batch, descs[i % pools], s)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    attn_ms = sum(a.elapsed_time(b) for a, b in evs) / steps
+    fl, kvb = rb.flops(), rb.decode_kv_bytes()
+    t_roof = kvb / (HBM_PEAK_GBS * 1e9) + fl / (MFMA_PEAK_TFLOPS * 1e12)
+    return {"config": name, "seqs": seqs, "tokens": rb.M, "ms_per_step": round(ms, 5),
+            "tokens_per_s": round(rb.M / (ms * 1e-3), 1), "attn_ms": round(attn_ms, 5),
+            "prefill_flops": fl, "decode_kv_bytes": kvb, "t_roof_ms": round(t_roof * 1e3, 5),
+            "roof_frac": round(t_roof / (attn_ms * 1e-3), 4)}
+
+
 def cpu_baseline(batch, budget_s=20.0):
     """Reference CPU attention (oracle/_ref: src/ref/ops.cpp attention_token) on the GPU batch's own
     pages, single-threaded. Sequences are timed one after another until the budget is spent."""
@@ -189,6 +223,12 @@ def main():
         extra[name]["sum_ctx"] = sum(r["ctxs"])
     if not only or "prefill" in only:
         extra["prefill_2048_on_6000"] = prefill_config(max(10, args.steps // 5), 3)
+    if not only or "mixed" in only:
+        from q38a.workloads import mixed_seqs
+        extra["mixed_512_plus_7"] = ragged_config("mixed_512_plus_7", mixed_seqs(0), max(10, args.steps // 2), 3)
+    if not only or "prefill_ragged" in only:
+        extra["prefill_2048_on_6000_ragged"] = ragged_config("prefill_2048_on_6000_ragged", [(6000, 2048)],
+                                                             max(10, args.steps // 5), 3, pools=1)
     batch = head.pop("_batch")
     cpu = None if args.no_cpu else cpu_baseline(batch)
     line = {

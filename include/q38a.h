@@ -145,8 +145,15 @@ int q38a_attention_decode(const q38a_attention_params* p, const q38a_batch_desc*
 int q38a_attention_prefill(const q38a_attention_params* p, const q38a_batch_desc* batch,
                            const q38a_kv_cache_desc* kv, void* stream);
 
+/* Floats of split_scratch q38a_attention_ragged needs for a batch of these host sizes (the
+ * BatchDesc host fields, num_seqs/num_tokens/max_tokens_per_seq, of every launch it serves must
+ * not exceed them). No counterpart in the reference; 0 for invalid arguments. */
+size_t q38a_ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int num_q_heads,
+                                  int num_kv_heads, int max_splits);
+
 /* Mixed continuous-batching step: sequences with one token (decode rows) and with several
- * (prefill chunks) in one ragged batch, scheduled by one attention launch plus the split merge.
+ * (prefill chunks) in one ragged batch, scheduled by one attention launch plus the split merge;
+ * split_scratch holds q38a_ragged_scratch_floats(...) floats.
  * No counterpart in the reference (its Engine::step, src/engine.cpp:133-182, runs prefill and
  * decode as separate launches); semantics are those of attention_decode / attention_prefill
  * applied to each sequence. */

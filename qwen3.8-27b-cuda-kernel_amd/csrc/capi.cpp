@@ -20,6 +20,7 @@ int launch_attention_prefill(const q38a_attention_params& p, const q38a_batch_de
 int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
                             hipStream_t stream);
 int max_group();
+size_t ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits);
 
 namespace {
 thread_local std::string g_error;
@@ -195,6 +196,14 @@ int q38a_attention_decode_splits(int batch_seqs, int kv_heads, int num_sms, int 
 size_t q38a_split_scratch_floats(int rows, int num_q_heads, int max_splits) {
   if (rows <= 0 || num_q_heads <= 0 || max_splits <= 0) return 0;
   return size_t(rows) * size_t(num_q_heads) * size_t(max_splits) * (kHeadDim + 2);
+}
+
+size_t q38a_ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int num_q_heads,
+                                  int num_kv_heads, int max_splits) {
+  if (num_seqs <= 0 || num_tokens <= 0 || max_tokens_per_seq <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads != 0 || max_splits <= 0)
+    return 0;
+  return ragged_scratch_floats(num_seqs, num_tokens, max_tokens_per_seq, num_q_heads, num_kv_heads, max_splits);
 }
 
 int q38a_attention_decode(const q38a_attention_params* p, const q38a_batch_desc* batch,

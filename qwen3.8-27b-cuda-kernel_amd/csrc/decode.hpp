@@ -1,0 +1,492 @@
+// Split-KV flash-decoding over the paged KV cache on gfx950 MFMA, plus the gated split merge.
+//
+// Semantics follow reference src/kernels/attention_decode.cu:97-257 (and the exact CPU form
+// src/ref/ops.cpp:144-171): for decode row b and q head hq (kv head hq / group), softmax over keys
+// [0, seq_pos0[b] + 1) of q.k / 16, weighted sum of V, then out = (acc / l) * sigmoid(gate) in bf16.
+//
+// MI355X design. Decode is HBM-bound (each KV byte is used once); with GQA 6 and int8 KV it needs
+// ~12 flop/byte, which at 8 TB/s is more than the non-packed fp32 VALU can issue alongside the
+// int8 widening, so both products run on MFMA and the VALU only widens codes and runs the softmax:
+//   * one workgroup = 4 waves works on one item (sequence, kv head, run of whole pages, see
+//     plan.hpp); each wave takes 16-token blocks of the item's pages in turn;
+//   * S^T[16 tok][16 heads] = K[16 tok][256] . Q^T with v_mfma_f32_16x16x32_f16: K codes enter the
+//     MFMA exactly (int8 -> fp16 by a byte permute and one packed add), Q as stored (fp16), and the
+//     per-(token, 64-dim group) K scale multiplies the four group partials in fp32 afterwards;
+//   * O[16 heads][256] += P'[16 heads][16 tok] . V[16 tok][256] with v_mfma_f32_16x16x16_f16:
+//     V codes are exact in fp16 and the V scale is folded into P' = p * v_scale per group, so no
+//     dequantised value is ever rounded; P' (<= 65504 since p <= 1) enters as an fp16 pair
+//     hi + lo (two MFMAs), i.e. with a 22-bit significand;
+//   * each wave keeps the next block's loads in flight while it computes the current one;
+//   * the S^T accumulator layout (lane = head, 4 tokens) is exactly the A-operand layout of the
+//     PV product, so probabilities never leave registers;
+//   * K rows are read as 4 x 16-byte loads per lane (a 16-lane group covers 64 contiguous bytes of
+//     a row), V rows as 16 x 4-byte loads (16 lanes cover 64 contiguous bytes);
+//   * the 4 waves' (max, sum, acc) are merged in LDS and written once per item as a partial;
+//     attn_merge_kernel combines partials with the log-sum-exp rule and applies sigmoid(gate).
+// bf16 KV pages use the same schedule with bf16 MFMAs for both products; q (fp16) is split exactly
+// into two bf16 operands and P likewise into hi + lo.
+#pragma once
+
+#include "plan.hpp"
+
+namespace q38a {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxGroup = 8;
+constexpr int kQStride = kHeadDim + 8;  // LDS row stride of q (halves): rows land on distinct banks
+constexpr int kMaxMergeSplits = 512;  // max_splits accepted by the launchers
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int nq, nkv, group;
+  int attn_layer;
+  float* scratch;
+  int max_splits;
+  int target_items;
+  const uint16_t* gate;  // bf16, row stride ld_gate
+  int ld_gate;
+  uint16_t* out;         // [M][nq * 256] bf16
+};
+
+
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+// 16-byte register vector (a native vector type, so copies never go through memory)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Four int8 codes -> two fp16 pairs, exactly: byte b -> fp16 bits 0x64 | (b ^ 0x80) = 1024 + (c + 128),
+// then subtract 1152. One XOR per word, one byte permute and one packed add per pair.
+__device__ inline void codes4_to_half(uint32_t w, half2_t& lo, half2_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [b0, 64, b1, 64]
+  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [b2, 64, b3, 64]
+  const half2_t bias = {_Float16(1152.0f), _Float16(1152.0f)};
+  lo = __builtin_bit_cast(half2_t, a) - bias;
+  hi = __builtin_bit_cast(half2_t, b) - bias;
+}
+
+__device__ inline half8_t codes16_to_half8(uint32_t w0, uint32_t w1) {
+  half2_t a, b, c, d;
+  codes4_to_half(w0, a, b);
+  codes4_to_half(w1, c, d);
+  return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Byte i of two words (codes of tokens r and r + 1 at one dim) -> fp16 pair, exactly.
+__device__ inline half2_t code_pair_to_half(uint32_t w_r0, uint32_t w_r1, int i) {
+  const uint32_t sel = 0x0C000C00u | (uint32_t(4 + i) << 16) | uint32_t(i);  // [b_r0, 0, b_r1, 0]
+  const uint32_t x = __builtin_amdgcn_perm(w_r1, w_r0, sel) ^ 0x64806480u;
+  const half2_t bias = {_Float16(1152.0f), _Float16(1152.0f)};
+  return __builtin_bit_cast(half2_t, x) - bias;
+}
+
+__device__ inline float half_lo(uint32_t w) { return float(__builtin_bit_cast(_Float16, uint16_t(w))); }
+__device__ inline float half_hi(uint32_t w) { return float(__builtin_bit_cast(_Float16, uint16_t(w >> 16))); }
+
+__device__ inline short bf16_short(float f) { return short(bf16_bits(f)); }
+
+// x = hi + lo with hi = bf16(x) and lo = bf16(x - hi): a 16-bit significand carried by two bf16
+// MFMA operands (relative error ~2^-17 instead of bf16's 2^-9), with fp32's exponent range.
+__device__ inline void split_bf16(float x, short& hi, short& lo) {
+  const uint16_t h = bf16_bits(x);
+  hi = short(h);
+  lo = short(bf16_bits(x - bf16_value(h)));
+}
+
+// Online-softmax state update shared by both page formats. S holds this lane's 4 raw scores
+// (head n16, tokens 4 j4 + r); returns p[4] and rescales O when the running max moved.
+__device__ inline void softmax_step(const float (&S)[4], const bool (&valid)[4], float& m_run, float& l_run,
+                                    float (&p)[4], float4_t (&O)[16], int j4) {
+  float s2[4], bmax = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    s2[r] = valid[r] ? S[r] * kScoreScale : -INFINITY;
+    bmax = fmaxf(bmax, s2[r]);
+  }
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+  const float mnew = fmaxf(m_run, bmax);
+  const float corr = exp2f(m_run - mnew);
+  float psum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p[r] = exp2f(s2[r] - mnew);
+    psum += p[r];
+  }
+  l_run = l_run * corr + psum;
+  m_run = mnew;
+  if (__any(corr != 1.0f)) {
+    // O rows are heads 4 j4 + r; their correction factors live in lanes 4 j4 + r (quad 0)
+    float cr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * j4 + r, 64);
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) O[k][r] *= cr[r];
+  }
+}
+
+// scale of (token r, group g) from a 32-byte [token][group] fp16 block
+__device__ inline float scale_at(const u32x4 (&sc)[2], int r, int g) {
+  const int idx = r * 4 + g;
+  const u32x4 w = sc[idx >> 3];
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t word = ws[(idx & 7) >> 1];
+  return (idx & 1) ? half_hi(word) : half_lo(word);
+}
+
+struct Int8Block {
+  u32x4 k[4];         // K codes of token t0 + n16, dims 64g + 16 j4 + [0, 16), g = 0..3
+  u32x4 ks[2];        // K scales of tokens t0 + 4 j4 + [0, 4): [token][group] fp16
+  uint32_t v[4][4];   // [g][r]: V codes of token t0 + 4 j4 + r, dims 64g + 4 n16 + [0, 4)
+  u32x4 vs[2];        // V scales of tokens t0 + 4 j4 + [0, 4)
+};
+
+__device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, const PageLayout& L, int kvh, int in0,
+                                       int n16, int j4) {
+  const uint8_t* krow = pg + L.k_row(kvh, in0 + n16);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) d.k[g] = *reinterpret_cast<const u32x4*>(krow + 64 * g + 16 * j4);
+  const u32x4* ksp = reinterpret_cast<const u32x4*>(pg + L.k_scales(kvh, in0 + 4 * j4));
+  d.ks[0] = ksp[0];
+  d.ks[1] = ksp[1];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint8_t* vrow = pg + L.v_row(kvh, in0 + 4 * j4 + r);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) d.v[g][r] = *reinterpret_cast<const uint32_t*>(vrow + 64 * g + 4 * n16);
+  }
+  const u32x4* vsp = reinterpret_cast<const u32x4*>(pg + L.v_scales(kvh, in0 + 4 * j4));
+  d.vs[0] = vsp[0];
+  d.vs[1] = vsp[1];
+}
+
+// One 16-token block of int8 pages for this lane: S^T = K . Q^T per 64-dim group on fp16 MFMAs
+// (codes exact in fp16, q as stored), the group's K scale applied to the fp32 partial; then
+// O += P' V with P' = p * v_scale per group as an exact-sum fp16 pair hi + lo.
+__device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][2], const bool (&valid)[4],
+                                     float& m_run, float& l_run, float4_t (&O)[16], int j4) {
+  float S[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const half8_t q0 = qf[g][0];
+    const half8_t q1 = qf[g][1];
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes16_to_half8(d.k[g].x, d.k[g].y), q0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes16_to_half8(d.k[g].z, d.k[g].w), q1, acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[r] += acc[r] * scale_at(d.ks, r, g);
+  }
+  float p[4];
+  softmax_step(S, valid, m_run, l_run, p, O, j4);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    half4_t pa_hi, pa_lo;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = valid[r] ? p[r] * scale_at(d.vs, r, g) : 0.f;
+      const _Float16 h = _Float16(x);
+      pa_hi[r] = h;
+      pa_lo[r] = _Float16(x - float(h));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const half2_t v01 = code_pair_to_half(d.v[g][0], d.v[g][1], i);
+      const half2_t v23 = code_pair_to_half(d.v[g][2], d.v[g][3], i);
+      const half4_t vb = {v01[0], v01[1], v23[0], v23[1]};
+      O[4 * g + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa_hi, vb, O[4 * g + i], 0, 0, 0);
+      O[4 * g + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa_lo, vb, O[4 * g + i], 0, 0, 0);
+    }
+  }
+}
+
+// int8 pages: keys [t_begin, t_end); wave w takes the 16-token blocks t_begin + 16 (w + 4k) and keeps
+// the next block's loads in flight while it computes the current one. Block indices, pages and
+// block-table reads are wave-uniform.
+__device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, const uint16_t* qs,
+                                 int t_begin, int t_end, float& m_run, float& l_run, float4_t (&O)[16]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15, j4 = lane >> 4;
+  // Q^T operand rows in LDS (zero rows past the group): lane (head n16, k-group j4) reads dims
+  // 64g + 16 j4 + 8h + [0, 8) for group g, half h
+  const uint16_t* qlane = qs + n16 * kQStride + 16 * j4;
+  const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
+  auto page_of = [&](int t0) { return layer + size_t(bt[t0 / kPageTokens]) * kv.page_bytes; };
+  auto load_q = [&](half8_t (&qf)[4][2]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) qf[g][h] = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
+  };
+  half8_t qf[4][2];
+  load_q(qf);
+  auto run = [&](const Int8Block& d, int t0) {
+    bool valid[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) valid[r] = t0 + 4 * j4 + r < t_end;
+    compute_block(d, qf, valid, m_run, l_run, O, j4);
+  };
+  Int8Block cur, nxt;
+  const int step = 16 * kWaves;
+  int t0 = t_begin + 16 * wave;
+  if (t0 < t_end) load_int8_block(cur, page_of(t0), kv.layout, kvh, t0 % kPageTokens, n16, j4);
+  for (; t0 < t_end; t0 += step) {
+    const int t1 = t0 + step;
+    if (t1 < t_end) load_int8_block(nxt, page_of(t1), kv.layout, kvh, t1 % kPageTokens, n16, j4);
+    run(cur, t0);
+    cur = nxt;
+  }
+}
+
+// bf16 pages: keys [t_begin, t_end), each wave takes 16-token blocks in turn from global memory.
+__device__ void decode_item_bf16(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, int q_row,
+                                 int t_begin, int t_end, float& m_run, float& l_run, float4_t (&O)[16]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15, j4 = lane >> 4;
+  const int G = a.group;
+  const bool real = n16 < G;
+  const uint16_t* qrow = a.q + (size_t(q_row) * a.nq + kvh * G + (real ? n16 : 0)) * kHeadDim;
+  const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
+  const int nblk = (t_end - t_begin + 15) >> 4;
+  // bf16 pages: q (fp16) = hi + lo exactly, both bf16; P likewise split into hi + lo
+  bf16x8_t qb[4][2], qb_lo[4][2];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 w = *reinterpret_cast<const u32x4*>(qrow + 64 * g + 16 * j4 + 8 * h);
+      if (!real) w = u32x4{0u, 0u, 0u, 0u};
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+      bf16x8_t v, vl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (e & 1) ? half_hi(ws[e >> 1]) : half_lo(ws[e >> 1]);
+        short hi, lo;
+        split_bf16(x, hi, lo);
+        v[e] = __builtin_bit_cast(__bf16, hi);
+        vl[e] = __builtin_bit_cast(__bf16, lo);
+      }
+      qb[g][h] = v;
+      qb_lo[g][h] = vl;
+    }
+  for (int blk = wave; blk < nblk; blk += kWaves) {
+    const int t0 = t_begin + 16 * blk;
+    const uint8_t* pg = layer + size_t(bt[t0 / kPageTokens]) * kv.page_bytes;
+    const int in0 = t0 % kPageTokens;
+    bool valid[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) valid[r] = t0 + 4 * j4 + r < t_end;
+    const uint8_t* krow = pg + kv.layout.k_row(kvh, in0 + n16);
+    u32x4 kw[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) kw[g][h] = *reinterpret_cast<const u32x4*>(krow + 2 * (64 * g + 16 * j4 + 8 * h));
+    // V: tile k, column n16 <-> dim 16 n16 + k; lane reads 32 contiguous bytes of each of 4 rows
+    u32x4 vw[4][2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint8_t* vrow = pg + kv.layout.v_row(kvh, in0 + 4 * j4 + r);
+      vw[r][0] = *reinterpret_cast<const u32x4*>(vrow + 32 * n16);
+      vw[r][1] = *reinterpret_cast<const u32x4*>(vrow + 32 * n16 + 16);
+    }
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bf16x8_t kb = __builtin_bit_cast(bf16x8_t, kw[g][h]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qb[g][h], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qb_lo[g][h], acc, 0, 0, 0);
+      }
+    const float S[4] = {acc[0], acc[1], acc[2], acc[3]};
+    float p[4];
+    softmax_step(S, valid, m_run, l_run, p, O, j4);
+    short4_t pa_hi, pa_lo;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      short hi, lo;
+      split_bf16(p[r], hi, lo);
+      pa_hi[r] = hi;
+      pa_lo[r] = lo;
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      short4_t vb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const u32x4 w = vw[r][k >> 3];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        const uint32_t word = ws[(k & 7) >> 1];
+        vb[r] = valid[r] ? short((k & 1) ? (word >> 16) : (word & 0xffffu)) : short(0);
+      }
+      O[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa_hi, vb, O[k], 0, 0, 0);
+      O[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa_lo, vb, O[k], 0, 0, 0);
+    }
+  }
+}
+
+// Dim of accumulator tile k, column n (depends on how V rows were mapped onto MFMA columns).
+template <int DT>
+__device__ inline int tile_dim(int k, int n) {
+  if constexpr (DT == Q38A_KV_INT8) return 64 * (k >> 2) + 4 * n + (k & 3);
+  else return 16 * n + k;
+}
+
+struct WaveMerge {
+  float m[kWaves][kMaxGroup];
+  float l[kWaves][kMaxGroup];
+  float o[kWaves][kMaxGroup][kHeadDim];
+};
+
+struct alignas(16) DecodeShared {
+  uint16_t q[16][kQStride];  // the item's q rows (fp16), rows past the group zero
+  WaveMerge merge;           // the 4 waves' state at the end of an item
+};
+
+// Merges the 4 waves' (m, l, O) of an item in LDS and writes the item's partial to scratch.
+template <int DT>
+__device__ void finish_item(const DecodeArgs& a, WaveMerge& sm, int b, int kvh, int split, float m_run, float l_run,
+                            const float4_t (&O)[16]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = a.group;
+  l_run += __shfl_xor(l_run, 16, 64);  // l over the 4 quads of each head lane
+  l_run += __shfl_xor(l_run, 32, 64);
+  if (lane < G) {
+    sm.m[wave][lane] = m_run;
+    sm.l[wave][lane] = l_run;
+  }
+  const int n16 = lane & 15, j4 = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int head = 4 * j4 + r;
+    if (head < G) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sm.o[wave][head][tile_dim<DT>(k, n16)] = O[k][r];
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kThreads) {
+    const int g = idx / kHeadDim, d = idx % kHeadDim;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm.m[w][g]);
+    float acc = 0.f, lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = sm.m[w][g] == -INFINITY ? 0.f : exp2f(sm.m[w][g] - M);
+      acc += f * sm.o[w][g][d];
+      lsum += f * sm.l[w][g];
+    }
+    float* dst = a.scratch + ((size_t(b) * a.nq + kvh * G + g) * a.max_splits + split) * (kHeadDim + 2);
+    dst[d] = acc;
+    if (d == 0) {
+      dst[kHeadDim] = M;
+      dst[kHeadDim + 1] = lsum;
+    }
+  }
+  __syncthreads();
+}
+
+// Persistent loop over the decode items of a launch: this workgroup is number `wg` of `nwg` that
+// stride over items; `plan` must hold build_plan's result. Partials go to a.scratch.
+template <int DT>
+__device__ __attribute__((always_inline)) inline void decode_items(const DecodeArgs& a, const BatchArgs& batch,
+                                                                   const KvArgs& kv, const PlanShared& plan,
+                                                                   DecodeShared& sh, int wg, int nwg) {
+  const int B = batch.num_seqs;
+  const int total = __builtin_amdgcn_readfirstlane(plan.prefix[B]);
+  const int cp = __builtin_amdgcn_readfirstlane(plan.chunk_pages);
+  for (int item = wg; item < total; item += nwg) {
+    const int b = __builtin_amdgcn_readfirstlane(find_seq(plan, B, item));  // LDS-derived, but uniform
+    const int local = item - __builtin_amdgcn_readfirstlane(plan.prefix[b]);
+    const int split = local / a.nkv, kvh = local % a.nkv;
+    const int L = decode_len(batch, b);
+    const int t_begin = split * cp * kPageTokens;
+    const int t_end = min(L, t_begin + cp * kPageTokens);
+    const int* bt = kv.block_table + size_t(batch.seq_slot[b]) * kv.max_pages_per_seq;
+    const int q_row = batch.seq_start[b];
+    float m_run = -INFINITY, l_run = 0.f;
+    float4_t O[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) O[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (DT == Q38A_KV_INT8) {
+      // stage the item's q rows (the previous item's last barrier protects the buffer)
+      for (int c = threadIdx.x; c < 16 * (kHeadDim / 8); c += kThreads) {
+        const int h = c / (kHeadDim / 8), c8 = (c % (kHeadDim / 8)) * 8;
+        u32x4 w = u32x4{0u, 0u, 0u, 0u};
+        if (h < a.group) w = *reinterpret_cast<const u32x4*>(a.q + (size_t(q_row) * a.nq + kvh * a.group + h) * kHeadDim + c8);
+        *reinterpret_cast<u32x4*>(&sh.q[h][c8]) = w;
+      }
+      __syncthreads();
+      decode_item_int8(a, kv, bt, kvh, &sh.q[0][0], t_begin, t_end, m_run, l_run, O);
+    } else {
+      decode_item_bf16(a, kv, bt, kvh, q_row, t_begin, t_end, m_run, l_run, O);
+    }
+    finish_item<DT>(a, sh.merge, b, kvh, split, m_run, l_run, O);
+  }
+}
+
+struct MergeShared {
+  float w[kMaxMergeSplits], l[kMaxMergeSplits];
+  float red[kHeadDim / 64];
+};
+
+// Combines the `splits` partials at src (split s at src + s * stride: acc[256], m, l) of one
+// (row, q head) with the log-sum-exp rule, normalises, applies sigmoid(gate) and stores bf16; 256 threads, thread = dim.
+// All splits' (m, l) are fetched at once, then each thread streams the splits with eight
+// independent loads in flight.
+__device__ inline void merge_row(const float* src, int splits, size_t stride, float gate_bf16_value,
+                                 uint16_t* out_row, MergeShared& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float mloc = -INFINITY;
+  for (int s = tid; s < splits; s += kHeadDim) {
+    const float m = src[s * stride + kHeadDim];
+    sh.w[s] = m;
+    sh.l[s] = src[s * stride + kHeadDim + 1];
+    mloc = fmaxf(mloc, m);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off, 64));
+  if (lane == 0) sh.red[wave] = mloc;
+  __syncthreads();
+  float M = sh.red[0];
+#pragma unroll
+  for (int w = 1; w < kHeadDim / 64; ++w) M = fmaxf(M, sh.red[w]);
+  __syncthreads();
+  float lloc = 0.f;
+  for (int s = tid; s < splits; s += kHeadDim) {
+    const float w = sh.w[s] == -INFINITY ? 0.f : exp2f(sh.w[s] - M);
+    sh.w[s] = w;
+    lloc += w * sh.l[s];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lloc += __shfl_xor(lloc, off, 64);
+  if (lane == 0) sh.red[wave] = lloc;
+  __syncthreads();
+  float lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kHeadDim / 64; ++w) lsum += sh.red[w];
+  const int d = tid;
+  float acc = 0.f;
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(s + u) * stride + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += sh.w[s + u] * v[u];
+  }
+  for (; s < splits; ++s) acc += sh.w[s] * src[s * stride + d];
+  const float y = (acc / lsum) * (1.0f / (1.0f + expf(-gate_bf16_value)));
+  out_row[d] = bf16_bits(y);
+}
+
+}  // namespace
+}  // namespace q38a

@@ -1,0 +1,218 @@
+// Mixed continuous-batching attention (q38a_attention_ragged): decode rows (sequences with one new
+// token) and prefill chunks (several new tokens) of one ragged batch in a single attention launch,
+// followed by one merge launch.
+//
+// Semantics are those of attention_decode (reference src/kernels/attention_decode.cu:97-257) for the
+// decode rows and attention_prefill (src/kernels/attention_prefill.cu:154-313) for the chunks; the
+// reference runs them as separate launches (src/engine.cpp:133-182).
+//
+// Launch layout: grid = P prefill workgroups followed by D = 2 x CUs decode workgroups, all 256
+// threads with the same register and LDS budget, so both kinds share the CUs. Workgroups are
+// dispatched in index order, so the long prefill units start first and the short, HBM-bound decode
+// items fill in behind them.
+//   * prefill: every (row tile, kv head) of a chunk is cut into parts of about the same number of key
+//     blocks (plan.hpp build_prefill_plan) so that a 512-token chunk still spreads over the whole
+//     chip; a tile with one part stores its final output, otherwise each part stores an
+//     unnormalised partial;
+//   * decode: the persistent split-KV loop of attention_decode over the decode rows' items;
+//   * merge: one workgroup per (decode row, q head) and one per 16 rows of each split prefill tile.
+// The plan is recomputed on the device from seq_start / seq_pos0 (graph-capturable); the first
+// workgroup of each kind records what the merge needs in the scratch header.
+//
+// Scratch (floats, q38a_ragged_scratch_floats): header (kHeaderInts ints) | decode partials
+// [B][nq][max_splits][258] | prefill partials [units][128 rows][258].
+#include "decode.hpp"
+#include "prefill.hpp"
+
+namespace q38a {
+namespace {
+
+constexpr int kPrefillTarget = 512;  // prefill units aimed for per launch (2 per CU on MI355X)
+constexpr int kMinChunk = 16;        // key blocks per part at least (512 keys)
+constexpr int kMergeRows = 16;       // prefill rows per merge workgroup
+constexpr int kHeaderInts = 4096;
+// header: [0] decode pages per item, [1] prefill key blocks per part,
+//         [kTaskPrefix + b] merge tasks (split tile, kv head) before sequence b,
+//         [kUnitPrefix + b] prefill units before sequence b, [kParts + b] parts per tile
+constexpr int kTaskPrefix = 4;
+constexpr int kUnitPrefix = kTaskPrefix + kMaxSeqs + 1;
+constexpr int kParts = kUnitPrefix + kMaxSeqs + 1;
+static_assert(kParts + kMaxSeqs <= kHeaderInts, "ragged scratch header");
+
+struct RaggedArgs {
+  int prefill_blocks;
+  int* header;
+  float* prefill_partials;
+};
+
+__device__ inline int parts_of(const BatchArgs& batch, int s, int chunk) {
+  const int n = prefill_len(batch, s);
+  return n ? prefill_parts(prefill_key_blocks(batch, s, n), chunk) : 0;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads, 2)
+    attn_ragged_kernel(RaggedArgs r, DecodeArgs d, PrefillArgs pa, BatchArgs batch, KvArgs kv) {
+  static_assert(kThreads == kPThreads && kThreads == kPlanThreads, "one block shape for both kinds");
+  __shared__ PlanShared plan;
+  __shared__ union alignas(16) Work {
+    KvTile tiles[2];
+    DecodeShared dec;
+  } sh;
+  const int B = batch.num_seqs;
+  if (int(blockIdx.x) < r.prefill_blocks) {
+    if constexpr (DT == Q38A_KV_INT8) {
+      build_prefill_plan(batch, pa.group, pa.nkv, kPrefillTarget, kMinChunk, plan);
+      const int chunk = plan.chunk_pages;
+      if (blockIdx.x == 0) {  // what the merge needs: parts, unit and merge-task offsets per sequence
+        int tasks[kPlanPer];
+#pragma unroll
+        for (int i = 0; i < kPlanPer; ++i) {
+          const int s = threadIdx.x * kPlanPer + i;
+          const int parts = s < B ? parts_of(batch, s, chunk) : 0;
+          tasks[i] = parts > 1 ? prefill_tiles(prefill_len(batch, s), pa.group) * pa.nkv : 0;
+          if (s < B) r.header[kParts + s] = parts;
+          if (s <= B) r.header[kUnitPrefix + s] = plan.prefix[s];
+        }
+        if (threadIdx.x == 0) r.header[1] = chunk;
+        block_scan_store(tasks, B, r.header + kTaskPrefix, plan);
+      }
+      const int u = blockIdx.x;
+      if (u >= plan.prefix[B]) return;
+      const int b = __builtin_amdgcn_readfirstlane(find_seq(plan, B, u));
+      const int local = u - plan.prefix[b];
+      const int n = prefill_len(batch, b);
+      const int parts = parts_of(batch, b, chunk);
+      const int tile_r = local / (pa.nkv * parts), rem = local % (pa.nkv * parts);
+      const int tile = prefill_tiles(n, pa.group) - 1 - tile_r;
+      prefill_unit(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts, parts,
+                   r.prefill_partials + size_t(u) * kPrefillRows * (kHeadDim + 2));
+    }
+  } else {
+    build_plan(batch, d.nkv, d.max_splits, d.target_items, plan);
+    const int wg = int(blockIdx.x) - r.prefill_blocks;
+    if (wg == 0 && threadIdx.x == 0) r.header[0] = plan.chunk_pages;
+    decode_items<DT>(d, batch, kv, plan, sh.dec, wg, int(gridDim.x) - r.prefill_blocks);
+  }
+}
+
+struct RaggedMergeArgs {
+  const uint16_t* gate;
+  int ld_gate;
+  uint16_t* out;
+  int nq, nkv, group;
+  const int* header;
+  const float* decode_partials;
+  const float* prefill_partials;
+  int max_splits;
+};
+
+// grid: B * nq decode blocks, then kPrefillRows / kMergeRows blocks per possible merge task.
+__global__ void __launch_bounds__(kHeadDim) attn_ragged_merge_kernel(RaggedMergeArgs a, BatchArgs batch) {
+  __shared__ MergeShared sh;
+  const int B = batch.num_seqs;
+  const int blk = blockIdx.x;
+  if (blk < B * a.nq) {
+    const int b = blk / a.nq, hq = blk % a.nq;
+    const int L = decode_len(batch, b);
+    if (L == 0) return;
+    const int row = batch.seq_start[b];
+    const float gt = bf16_value(a.gate[size_t(row) * a.ld_gate + hq * kHeadDim + threadIdx.x]);
+    const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), a.header[0]);
+    const float* src = a.decode_partials + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
+    merge_row(src, splits, kHeadDim + 2, gt, a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
+    return;
+  }
+  const int idx = blk - B * a.nq;
+  const int task = idx / (kPrefillRows / kMergeRows), grp = idx % (kPrefillRows / kMergeRows);
+  const int* tp = a.header + kTaskPrefix;
+  if (task >= tp[B]) return;
+  int lo = 0, hi = B - 1;  // sequence of the task: largest b with tp[b] <= task
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tp[mid] <= task) lo = mid;
+    else hi = mid - 1;
+  }
+  const int b = lo;
+  const int parts = a.header[kParts + b];
+  const int local = task - tp[b];
+  const int tile_r = local / a.nkv, kvh = local % a.nkv;
+  const int n = prefill_len(batch, b), G = a.group;
+  const int tile = prefill_tiles(n, G) - 1 - tile_r;
+  const size_t unit = size_t(a.header[kUnitPrefix + b]) + size_t(tile_r * a.nkv + kvh) * parts;
+  const size_t unit_floats = size_t(kPrefillRows) * (kHeadDim + 2);
+  for (int i = 0; i < kMergeRows; ++i) {
+    const int rt = kMergeRows * grp + i;  // row within the tile
+    const int row = kPrefillRows * tile + rt;
+    if (row >= n * G) break;
+    const int tok = row / G, hq = kvh * G + row % G;
+    const size_t m = size_t(batch.seq_start[b] + tok);
+    const float gt = bf16_value(a.gate[m * a.ld_gate + hq * kHeadDim + threadIdx.x]);
+    merge_row(a.prefill_partials + unit * unit_floats + size_t(rt) * (kHeadDim + 2), parts, unit_floats, gt,
+              a.out + (m * a.nq + hq) * kHeadDim, sh);
+    __syncthreads();  // sh is reused by the next row
+  }
+}
+
+struct RaggedShape {
+  size_t decode_floats, tasks_bound, units_bound;
+};
+
+RaggedShape ragged_shape(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits) {
+  RaggedShape s{};
+  s.decode_floats = size_t(num_seqs) * nq * max_splits * (kHeadDim + 2);
+  if (max_tokens_per_seq > 1) {
+    const size_t G = size_t(nq / nkv);
+    // sum_b ceil(n_b G / 128) <= M G / 128 + B tiles per kv head; max(1, floor(kt / chunk)) parts per
+    // tile add at most kPrefillTarget units
+    s.tasks_bound = size_t(nkv) * ((size_t(num_tokens) * G) / kPrefillRows + size_t(num_seqs));
+    s.units_bound = s.tasks_bound + kPrefillTarget;
+  }
+  return s;
+}
+
+}  // namespace
+
+int decode_grid(int* grid, int* target_items);
+
+size_t ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits) {
+  const RaggedShape s = ragged_shape(num_seqs, num_tokens, max_tokens_per_seq, nq, nkv, max_splits);
+  return size_t(kHeaderInts) + s.decode_floats + s.units_bound * kPrefillRows * (kHeadDim + 2);
+}
+
+int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
+                            hipStream_t stream) {
+  if (b.num_seqs == 0 || b.num_tokens == 0) return Q38A_OK;
+  if (b.num_seqs >= kMaxSeqs) return set_error(Q38A_ERR_INVALID, "attention_ragged: at most %d sequences", kMaxSeqs - 1);
+  if (p.max_splits > kMaxMergeSplits)
+    return set_error(Q38A_ERR_INVALID, "attention_ragged: max_splits %d exceeds %d", p.max_splits, kMaxMergeSplits);
+  if (kv.dtype != Q38A_KV_INT8 && b.max_tokens_per_seq > 1)
+    return set_error(Q38A_ERR_UNSUPPORTED, "attention_ragged: prefill chunks over bf16 pages not built yet");
+  const int G = p.num_q_heads / p.num_kv_heads;
+  const RaggedShape s = ragged_shape(b.num_seqs, b.num_tokens, b.max_tokens_per_seq, p.num_q_heads, p.num_kv_heads,
+                                     p.max_splits);
+  int dgrid = 0, target = 0;
+  if (int rc = decode_grid(&dgrid, &target)) return rc;
+  int* header = reinterpret_cast<int*>(p.split_scratch);
+  float* dec = p.split_scratch + kHeaderInts;
+  float* pre = dec + s.decode_floats;
+  const int pblocks = int(s.units_bound);
+  RaggedArgs r{pblocks, header, pre};
+  DecodeArgs d{p.q, p.num_q_heads, p.num_kv_heads, G, p.attn_layer, dec, p.max_splits, target, p.gate, p.ld_gate,
+               p.out};
+  PrefillArgs pa{p.q, p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, p.attn_layer};
+  const dim3 grid(unsigned(pblocks + dgrid));
+  if (kv.dtype == Q38A_KV_INT8)
+    hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_INT8>, grid, dim3(kThreads), 0, stream, r, d, pa, to_args(b),
+                       to_args(kv));
+  else
+    hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_BF16>, grid, dim3(kThreads), 0, stream, r, d, pa, to_args(b),
+                       to_args(kv));
+  if (int rc = check_hip(hipGetLastError(), "attention_ragged launch")) return rc;
+  RaggedMergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, header, dec, pre, p.max_splits};
+  const size_t mblocks = size_t(b.num_seqs) * p.num_q_heads + s.tasks_bound * (kPrefillRows / kMergeRows);
+  hipLaunchKernelGGL(attn_ragged_merge_kernel, dim3(unsigned(mblocks)), dim3(kHeadDim), 0, stream, m, to_args(b));
+  return check_hip(hipGetLastError(), "attention_ragged merge launch");
+}
+
+}  // namespace q38a

@@ -81,6 +81,7 @@ _SIGS = {
     "q38a_qk_norm_rope_append": (_i, [ctypes.POINTER(QkNormRopeParams), _PBatch, _PKv, _p]),
     "q38a_attention_decode_splits": (_i, [_i, _i, _i, _i]),
     "q38a_split_scratch_floats": (_sz, [_i, _i, _i]),
+    "q38a_ragged_scratch_floats": (_sz, [_i, _i, _i, _i, _i, _i]),
     "q38a_attention_decode": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_attention_prefill": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_attention_ragged": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
@@ -130,6 +131,11 @@ def rope_table(pos_begin, count, theta=1e7, rotary_dim=64):
 
 def split_scratch_floats(rows, num_q_heads, max_splits):
     return lib.q38a_split_scratch_floats(rows, num_q_heads, max_splits)
+
+
+def ragged_scratch_floats(num_seqs, num_tokens, max_tokens_per_seq, num_q_heads, num_kv_heads, max_splits):
+    return lib.q38a_ragged_scratch_floats(num_seqs, num_tokens, max_tokens_per_seq, num_q_heads, num_kv_heads,
+                                          max_splits)
 
 
 def qk_norm_rope_append(params, batch, kv, stream=0):

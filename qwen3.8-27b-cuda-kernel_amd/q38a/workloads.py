@@ -124,6 +124,14 @@ def prefill_flops(seqs):
     return 4 * HD * NQ * pairs
 
 
+def mixed_seqs(seed=0):
+    """Config 4: one 512-token prefill chunk + 7 decode rows; all 8 contexts (the chunk's prefix
+    first) lognormal with median 8192 and sigma 1, rounded and clipped to [64, 65536]."""
+    rng = np.random.default_rng(seed)
+    ctx = np.clip(np.round(np.exp(np.log(8192) + rng.normal(0, 1, 8))), 64, 65536).astype(int)
+    return [(int(ctx[0]), 512)] + [(int(c), 1) for c in ctx[1:]]
+
+
 class RaggedBatch:
     """A continuous-batching step: sequences [(prefix, n)] (n == 1: decode row, n > 1: prefill
     chunk), pages of all sequences interleaved by one random permutation of the pool."""
@@ -164,8 +172,8 @@ class RaggedBatch:
         self.q16 = torch.empty((self.M, NQ * HD), dtype=torch.float16, device="cuda")
         self.out = torch.empty((self.M, NQ * HD), dtype=torch.bfloat16, device="cuda")
         self.max_splits = 256
-        self.scratch = torch.empty(q38a.split_scratch_floats(self.B, NQ, self.max_splits), dtype=torch.float32,
-                                   device="cuda")
+        self.scratch = torch.empty(q38a.ragged_scratch_floats(self.B, self.M, max(n for _, n in self.seqs), NQ, NKV,
+                                                              self.max_splits), dtype=torch.float32, device="cuda")
 
     kv_desc = DecodeBatch.kv_desc
     append_params = DecodeBatch.append_params
