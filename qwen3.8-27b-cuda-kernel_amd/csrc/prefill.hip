@@ -5,11 +5,13 @@
 namespace q38a {
 namespace {
 
-// grid (tiles_x, nkv, B); the tile index is reversed so the longest rows start first
+// grid (tiles_x * nkv, B): block x = (tile from last to first, kv head), so the longest rows start
+// first and the kv heads of one row tile are dispatched together
 __global__ void __launch_bounds__(kPThreads, 2) attn_prefill_kernel(PrefillArgs a, BatchArgs batch, KvArgs kv) {
   __shared__ KvTile tiles[2];
-  const int tile = int(gridDim.x) - 1 - int(blockIdx.x);
-  prefill_unit(a, batch, kv, tiles, blockIdx.z, blockIdx.y, tile, 0, 1, nullptr);
+  const int tiles_x = int(gridDim.x) / a.nkv;
+  const int tile = tiles_x - 1 - int(blockIdx.x) / a.nkv, kvh = int(blockIdx.x) % a.nkv;
+  prefill_unit(a, batch, kv, tiles, blockIdx.y, kvh, tile, 0, 1, nullptr);
 }
 
 }  // namespace
@@ -21,7 +23,7 @@ int launch_attention_prefill(const q38a_attention_params& p, const q38a_batch_de
   const int G = p.num_q_heads / p.num_kv_heads;
   const int tiles_x = int((size_t(b.max_tokens_per_seq) * G + kRowsPerTile - 1) / kRowsPerTile);
   PrefillArgs a{p.q, p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, p.attn_layer};
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3(tiles_x, p.num_kv_heads, b.num_seqs), dim3(kPThreads), 0, stream, a,
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(tiles_x * p.num_kv_heads, b.num_seqs), dim3(kPThreads), 0, stream, a,
                      to_args(b), to_args(kv));
   return check_hip(hipGetLastError(), "attention_prefill launch");
 }

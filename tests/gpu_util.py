@@ -100,3 +100,30 @@ def paged_layout(rng, lengths, extra_pages=0):
         bt[b, :p] = perm[o:o + p]
         o += p
     return bt, total
+
+
+_hip = None
+
+
+def memcpy(dst, src, nbytes):
+    """Synchronous copy between raw addresses (host or device) through the HIP runtime torch loaded."""
+    global _hip
+    import ctypes
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        _hip.hipMemcpy.restype = ctypes.c_int
+    torch.cuda.synchronize()
+    rc = _hip.hipMemcpy(dst, src, nbytes, 4)  # hipMemcpyDefault
+    assert rc == 0, f"hipMemcpy failed: {rc}"
+
+
+def to_device_ptr(ptr, array):
+    a = np.ascontiguousarray(array)
+    memcpy(ptr, a.ctypes.data, a.nbytes)
+
+
+def from_device_ptr(ptr, shape, dtype):
+    a = np.empty(shape, dtype)
+    memcpy(a.ctypes.data, ptr, a.nbytes)
+    return a

@@ -13,8 +13,8 @@ import q38a
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
-    text = open(os.path.join(ROOT, "include", "q38a.h")).read()
+def declared_functions(header="q38a.h"):
+    text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(q38a_[a-z0-9_]+)\s*\(", text)))
 
@@ -26,6 +26,12 @@ def test_every_declared_symbol_is_exported():
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert set(q38a.EXPORTED) <= set(names)
+    from q38a import runtime
+    rt = declared_functions("q38a_runtime.h")
+    assert len(rt) >= 20
+    missing = [n for n in rt if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(runtime.EXPORTED) == set(rt)
 
 
 def test_page_layout_matches_reference_format():
@@ -94,3 +100,18 @@ def test_ragged_scratch_size_and_refusals():
     with pytest.raises(q38a.Q38AError, match="max_splits"):
         q38a.attention_ragged(q38a.AttentionParams(8, 8, 14336, 8, 24, 4, 0, 8, 600),
                               q38a.BatchDesc(2, 2, 1, 8, 8, 8, 8, 8), kv)
+
+
+def test_runtime_buckets_and_refusals():
+    from q38a import runtime
+    # reference src/model_runner.cpp:28-33: {1, 2, 4, 8, 12, 16, 24, 32, 48, 64} capped by max_batch
+    assert [runtime.bucket_for(n, 8) for n in range(1, 9)] == [1, 2, 4, 4, 8, 8, 8, 8]
+    assert [runtime.bucket_for(n, 64) for n in (9, 13, 17, 25, 33, 49, 64)] == [12, 16, 24, 32, 48, 64, 64]
+    assert runtime.bucket_for(10, 10) == 10
+    # bad options are refused before any device call
+    with pytest.raises(q38a.Q38AError, match="bad options"):
+        runtime.Runner(0, 0)
+    with pytest.raises(q38a.Q38AError, match="bad options"):
+        runtime.Runner(8, 8, num_q_heads=24, num_kv_heads=5)
+    with pytest.raises(q38a.Q38AError, match="bad options"):
+        runtime.Runner(8, 8, max_splits=513)
