@@ -144,6 +144,121 @@ def ragged_config(name, seqs, steps, warmup, pools=3):
             "roof_frac": round(t_roof / (attn_ms * 1e-3), 4)}
 
 
+def profile_workload(name, reps=20):
+    """The launches the rocprofv3 summaries under profiles/ are made from: 3 warm-up and `reps`
+    timed attention launches of one workload, then 4 passes of a plain copy kernel over known bytes
+    (y = -x on 1 GiB of fp32: 1 GiB read, 1 GiB written; no workload uses neg) that calibrate FETCH_SIZE and
+    WRITE_SIZE. Prints one line per phase."""
+    import torch
+    import q38a
+    from q38a.workloads import DecodeBatch, RaggedBatch, decode_contexts, mixed_seqs
+    s = torch.cuda.current_stream().cuda_stream
+    if name in ("decode_b8", "long_b8", "long_b1", "long_b8_bf16"):
+        dt = q38a.KV_BF16 if name.endswith("bf16") else q38a.KV_INT8
+        b = DecodeBatch(decode_contexts(name), dtype=dt, seed=0, pools=3)
+        ap, descs = b.attention_params(), [b.kv_desc(i) for i in range(3)]
+        q38a.qk_norm_rope_append(b.append_params(), b.batch, descs[0], s)
+        run = lambda i: q38a.attention_decode(ap, b.batch, descs[i % 3], s)  # noqa: E731
+    elif name == "prefill":
+        rb = RaggedBatch([(6000, 2048)], seed=0)
+        ap, kvd = rb.attention_params(), rb.kv_desc(0)
+        q38a.qk_norm_rope_append(rb.append_params(), rb.batch, kvd, s)
+        run = lambda i: q38a.attention_prefill(ap, rb.batch, kvd, s)  # noqa: E731
+    elif name == "mixed":
+        rb = RaggedBatch(mixed_seqs(0), seed=0, pools=3)
+        ap, descs = rb.attention_params(), [rb.kv_desc(i) for i in range(3)]
+        q38a.qk_norm_rope_append(rb.append_params(), rb.batch, descs[0], s)
+        run = lambda i: q38a.attention_ragged(ap, rb.batch, descs[i % 3], s)  # noqa: E731
+    else:
+        raise SystemExit(f"unknown profile workload {name}")
+    for i in range(3):
+        run(i)
+    torch.cuda.synchronize()
+    for i in range(reps):
+        run(i)
+    torch.cuda.synchronize()
+    print(f"profile {name}: {reps} attention launches", flush=True)
+    x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(4):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print("profile copy: 4 x (1 GiB read + 1 GiB written)", flush=True)
+
+
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)):
+        rows += list(csv.DictReader(open(f)))
+    if not rows:
+        raise SystemExit(f"no *{suffix} under {d}")
+    return rows
+
+
+def pmc_summary(fetch_dir, write_dir, out=None):
+    """Per-kernel mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch) from two rocprofv3 --pmc runs of
+    `bench.py --profile`, scaled by what the same counters read for the 1 GiB copy kernel."""
+    import collections
+    vals = collections.defaultdict(list)
+    for d, counter in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+        for r in _csv_rows(d, "counter_collection.csv"):
+            if r["Counter_Name"] == counter:
+                vals[(r["Kernel_Name"], counter)].append(float(r["Counter_Value"]))
+    names = sorted({k for k, _ in vals})
+    copy = [n for n in names if "neg_kernel" in n]
+    if not copy:
+        raise SystemExit("copy kernel not found")
+    gib_kib = float(1 << 20)
+    cf = gib_kib / (sum(vals[(copy[0], "FETCH_SIZE")]) / len(vals[(copy[0], "FETCH_SIZE")]))
+    cw = gib_kib / (sum(vals[(copy[0], "WRITE_SIZE")]) / len(vals[(copy[0], "WRITE_SIZE")]))
+    lines = [f"copy kernel: {copy[0][:80]}", f"scale FETCH_SIZE x {cf:.4f}, WRITE_SIZE x {cw:.4f} (1 GiB each way)",
+             "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled read MB | scaled write MB |",
+             "|---|---|---|---|---|---|"]
+    total = 0.0  # the attention launch: q38a attention and merge kernels
+    for n in names:
+        if n in copy:
+            continue
+        f, w = vals.get((n, "FETCH_SIZE"), [0.0]), vals.get((n, "WRITE_SIZE"), [0.0])
+        fm, wm = sum(f) / len(f), sum(w) / len(w)
+        rb, wb = fm * 1024 * cf, wm * 1024 * cw
+        if short_name(n).startswith("q38a::attn_"):
+            total += rb + wb
+        lines.append(f"| {short_name(n)} | {len(f)} | {fm:.0f} | {wm:.0f} | {rb / 1e6:.2f} | {wb / 1e6:.2f} |")
+    lines.append(f"traffic_bytes_per_launch: {total:.0f}")
+    text = "\n".join(lines)
+    print(text)
+    if out:
+        open(out, "w").write(text + "\n")
+
+
+def short_name(n):
+    n = n.replace("(anonymous namespace)::", "").replace("void ", "")
+    return n.split("(")[0][:80]
+
+
+def stats_summary(d):
+    """Kernel table of a rocprofv3 --kernel-trace --stats run (average durations in microseconds)."""
+    rows = _csv_rows(d, "kernel_stats.csv")
+    print("| kernel | calls | average us | min us | max us | share % |")
+    print("|---|---|---|---|---|---|")
+    for r in rows:
+        print(f"| {short_name(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+              f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} |")
+
+
+def read_traffic(workload):
+    """Scaled HBM bytes per attention launch from profiles/<workload>_traffic.txt, or None."""
+    path = os.path.join(ROOT, "profiles", f"attention_{workload}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(batch, budget_s=20.0):
     """Reference CPU attention (oracle/_ref: src/ref/ops.cpp attention_token) on the GPU batch's own
     pages, single-threaded. Sequences are timed one after another until the budget is spent."""
@@ -200,8 +315,17 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of configs to run (default: all)")
+    ap.add_argument("--only", default="", help="comma list of extra configs to run (default: all; "
+                                                "'headline' runs none)")
+    ap.add_argument("--profile", default="", help="run one workload's launches for rocprofv3 and exit")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--pmc-out", default=None)
+    ap.add_argument("--stats-summary", metavar="DIR")
     args = ap.parse_args()
+    if args.pmc_summary:
+        return pmc_summary(*args.pmc_summary, out=args.pmc_out)
+    if args.stats_summary:
+        return stats_summary(args.stats_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the single-GPU number is the reported value.", file=sys.stderr)
@@ -210,6 +334,8 @@ def main():
     import torch
     import q38a
     torch.cuda.init()
+    if args.profile:
+        return profile_workload(args.profile)
     only = set(filter(None, args.only.split(",")))
     extra = {}
     head = decode_config("decode_b8", q38a.KV_INT8, args.steps, args.warmup)
@@ -249,7 +375,7 @@ def main():
                                "24q/4kv heads, head_dim 256, int8 64-token pages",
                    "sum_ctx": sum(head["ctxs"]), "tokens_per_step": 8},
         "roofline": {"bound": "hbm", "achieved": round(head["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_b8"),
                      "kernel": "attention_decode (attn_decode_kernel + attn_merge_kernel)",
                      "kernel_ms": round(head["attn_ms"], 5)},
         "cpu_baseline": cpu,

@@ -13,9 +13,8 @@
 //     MFMA exactly (int8 -> fp16 by a byte permute and one packed add), Q as stored (fp16), and the
 //     per-(token, 64-dim group) K scale multiplies the four group partials in fp32 afterwards;
 //   * O[16 heads][256] += P'[16 heads][16 tok] . V[16 tok][256] with v_mfma_f32_16x16x16_f16:
-//     V codes are exact in fp16 and the V scale is folded into P' = p * v_scale per group, so no
-//     dequantised value is ever rounded; P' (<= 65504 since p <= 1) enters as an fp16 pair
-//     hi + lo (two MFMAs), i.e. with a 22-bit significand;
+//     V codes are exact in fp16 and the V scale is folded into P' = p * v_scale per group, rounded
+//     once to fp16 (relative error <= 2^-11, a twentieth of the output tolerance);
 //   * each wave keeps the next block's loads in flight while it computes the current one;
 //   * the S^T accumulator layout (lane = head, 4 tokens) is exactly the A-operand layout of the
 //     PV product, so probabilities never leave registers;
@@ -109,11 +108,11 @@ __device__ inline void softmax_step(const float (&S)[4], const bool (&valid)[4],
   bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
   bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
   const float mnew = fmaxf(m_run, bmax);
-  const float corr = exp2f(m_run - mnew);
+  const float corr = __builtin_amdgcn_exp2f(m_run - mnew);  // m_run = -inf gives 0
   float psum = 0.f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    p[r] = exp2f(s2[r] - mnew);
+    p[r] = __builtin_amdgcn_exp2f(s2[r] - mnew);
     psum += p[r];
   }
   l_run = l_run * corr + psum;
@@ -146,30 +145,45 @@ struct Int8Block {
   u32x4 vs[2];        // V scales of tokens t0 + 4 j4 + [0, 4)
 };
 
-__device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, const PageLayout& L, int kvh, int in0,
-                                       int n16, int j4) {
-  const uint8_t* krow = pg + L.k_row(kvh, in0 + n16);
+// Per-lane byte offsets of a block's loads, relative to the block's uniform bases (page + 256 *
+// first token for rows, page + 8 * first token for scales); fixed for the whole item.
+struct Int8Offsets {
+  uint32_t k, ks, v, vs;
+};
+
+__device__ inline Int8Offsets int8_offsets(const PageLayout& L, int kvh, int n16, int j4) {
+  Int8Offsets o;
+  o.k = uint32_t(L.k_row(kvh, n16)) + 16 * j4;
+  o.ks = uint32_t(L.k_scales(kvh, 4 * j4));
+  o.v = uint32_t(L.v_row(kvh, 4 * j4)) + 4 * n16;
+  o.vs = uint32_t(L.v_scales(kvh, 4 * j4));
+  return o;
+}
+
+// rows: page + 256 * in0; sc: page + 8 * in0 (in0 = the block's first token within its page)
+__device__ inline void load_int8_block(Int8Block& d, const uint8_t* rows, const uint8_t* sc, const Int8Offsets& o) {
 #pragma unroll
-  for (int g = 0; g < 4; ++g) d.k[g] = *reinterpret_cast<const u32x4*>(krow + 64 * g + 16 * j4);
-  const u32x4* ksp = reinterpret_cast<const u32x4*>(pg + L.k_scales(kvh, in0 + 4 * j4));
-  d.ks[0] = ksp[0];
-  d.ks[1] = ksp[1];
+  for (int g = 0; g < 4; ++g) d.k[g] = *reinterpret_cast<const u32x4*>(rows + o.k + 64 * g);
+  d.ks[0] = *reinterpret_cast<const u32x4*>(sc + o.ks);
+  d.ks[1] = *reinterpret_cast<const u32x4*>(sc + o.ks + 16);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const uint8_t* vrow = pg + L.v_row(kvh, in0 + 4 * j4 + r);
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) d.v[g][r] = *reinterpret_cast<const uint32_t*>(vrow + 64 * g + 4 * n16);
-  }
-  const u32x4* vsp = reinterpret_cast<const u32x4*>(pg + L.v_scales(kvh, in0 + 4 * j4));
-  d.vs[0] = vsp[0];
-  d.vs[1] = vsp[1];
+    for (int g = 0; g < 4; ++g) d.v[g][r] = *reinterpret_cast<const uint32_t*>(rows + o.v + kHeadDim * r + 64 * g);
+  d.vs[0] = *reinterpret_cast<const u32x4*>(sc + o.vs);
+  d.vs[1] = *reinterpret_cast<const u32x4*>(sc + o.vs + 16);
 }
 
 // One 16-token block of int8 pages for this lane: S^T = K . Q^T per 64-dim group on fp16 MFMAs
 // (codes exact in fp16, q as stored), the group's K scale applied to the fp32 partial; then
-// O += P' V with P' = p * v_scale per group as an exact-sum fp16 pair hi + lo.
-__device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][2], const bool (&valid)[4],
-                                     float& m_run, float& l_run, float4_t (&O)[16], int j4) {
+// O += P' V with P' = p * v_scale per group rounded once to fp16 (relative error <= 2^-11; V codes
+// are exact). Tail: the block may reach past the item's last key (masked).
+template <bool Tail>
+__device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][2], int t0, int t_end, float& m_run,
+                                     float& l_run, float4_t (&O)[16], int j4) {
+  bool valid[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) valid[r] = !Tail || t0 + 4 * j4 + r < t_end;
   float S[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -185,28 +199,22 @@ __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][
   softmax_step(S, valid, m_run, l_run, p, O, j4);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    half4_t pa_hi, pa_lo;
+    half4_t pa;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float x = valid[r] ? p[r] * scale_at(d.vs, r, g) : 0.f;
-      const _Float16 h = _Float16(x);
-      pa_hi[r] = h;
-      pa_lo[r] = _Float16(x - float(h));
-    }
+    for (int r = 0; r < 4; ++r) pa[r] = _Float16(valid[r] ? p[r] * scale_at(d.vs, r, g) : 0.f);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const half2_t v01 = code_pair_to_half(d.v[g][0], d.v[g][1], i);
       const half2_t v23 = code_pair_to_half(d.v[g][2], d.v[g][3], i);
       const half4_t vb = {v01[0], v01[1], v23[0], v23[1]};
-      O[4 * g + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa_hi, vb, O[4 * g + i], 0, 0, 0);
-      O[4 * g + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa_lo, vb, O[4 * g + i], 0, 0, 0);
+      O[4 * g + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, O[4 * g + i], 0, 0, 0);
     }
   }
 }
 
-// int8 pages: keys [t_begin, t_end); wave w takes the 16-token blocks t_begin + 16 (w + 4k) and keeps
-// the next block's loads in flight while it computes the current one. Block indices, pages and
-// block-table reads are wave-uniform.
+// int8 pages: keys [t_begin, t_end); wave w takes the 16-token blocks t_begin + 16 (w + 4k) and
+// keeps the next block's loads in flight while it computes the current one. Block indices, pages and block-table reads are wave-uniform; only the item's last block
+// is masked.
 __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, const uint16_t* qs,
                                  int t_begin, int t_end, float& m_run, float& l_run, float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63;
@@ -215,29 +223,31 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   // Q^T operand rows in LDS (zero rows past the group): lane (head n16, k-group j4) reads dims
   // 64g + 16 j4 + 8h + [0, 8) for group g, half h
   const uint16_t* qlane = qs + n16 * kQStride + 16 * j4;
-  const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
-  auto page_of = [&](int t0) { return layer + size_t(bt[t0 / kPageTokens]) * kv.page_bytes; };
-  auto load_q = [&](half8_t (&qf)[4][2]) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) qf[g][h] = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
-  };
   half8_t qf[4][2];
-  load_q(qf);
-  auto run = [&](const Int8Block& d, int t0) {
-    bool valid[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) valid[r] = t0 + 4 * j4 + r < t_end;
-    compute_block(d, qf, valid, m_run, l_run, O, j4);
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) qf[g][h] = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
+  const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
+  const Int8Offsets off = int8_offsets(kv.layout, kvh, n16, j4);
+  // the block table is read-only during the launch: through the constant address space its
+  // wave-uniform entries become scalar loads, which do not wait behind the vector loads in flight
+  const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
+  auto load = [&](Int8Block& d, int t) {
+    const uint8_t* pg = layer + size_t(btc[t / kPageTokens]) * kv.page_bytes;
+    const int in0 = t % kPageTokens;
+    load_int8_block(d, pg + in0 * kHeadDim, pg + in0 * 8, off);
+  };
+  auto run = [&](const Int8Block& d, int t) {
+    compute_block<true>(d, qf, t, t_end, m_run, l_run, O, j4);
   };
   Int8Block cur, nxt;
   const int step = 16 * kWaves;
   int t0 = t_begin + 16 * wave;
-  if (t0 < t_end) load_int8_block(cur, page_of(t0), kv.layout, kvh, t0 % kPageTokens, n16, j4);
+  if (t0 < t_end) load(cur, t0);
   for (; t0 < t_end; t0 += step) {
     const int t1 = t0 + step;
-    if (t1 < t_end) load_int8_block(nxt, page_of(t1), kv.layout, kvh, t1 % kPageTokens, n16, j4);
+    if (t1 < t_end) load(nxt, t1);
     run(cur, t0);
     cur = nxt;
   }

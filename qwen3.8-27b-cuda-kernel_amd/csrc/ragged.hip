@@ -15,7 +15,7 @@
 //     chip; a tile with one part stores its final output, otherwise each part stores an
 //     unnormalised partial;
 //   * decode: the persistent split-KV loop of attention_decode over the decode rows' items;
-//   * merge: one workgroup per (decode row, q head) and one per 16 rows of each split prefill tile.
+//   * merge: one workgroup per (decode row, q head) and one per row of each split prefill tile.
 // The plan is recomputed on the device from seq_start / seq_pos0 (graph-capturable); the first
 // workgroup of each kind records what the merge needs in the scratch header.
 //
@@ -29,7 +29,6 @@ namespace {
 
 constexpr int kPrefillTarget = 512;  // prefill units aimed for per launch (2 per CU on MI355X)
 constexpr int kMinChunk = 16;        // key blocks per part at least (512 keys)
-constexpr int kMergeRows = 16;       // prefill rows per merge workgroup
 constexpr int kHeaderInts = 4096;
 // header: [0] decode pages per item, [1] prefill key blocks per part,
 //         [kTaskPrefix + b] merge tasks (split tile, kv head) before sequence b,
@@ -107,7 +106,7 @@ struct RaggedMergeArgs {
   int max_splits;
 };
 
-// grid: B * nq decode blocks, then kPrefillRows / kMergeRows blocks per possible merge task.
+// grid: B * nq decode blocks, then one block per row of every possible merge task (kPrefillRows).
 __global__ void __launch_bounds__(kHeadDim) attn_ragged_merge_kernel(RaggedMergeArgs a, BatchArgs batch) {
   __shared__ MergeShared sh;
   const int B = batch.num_seqs;
@@ -124,7 +123,7 @@ __global__ void __launch_bounds__(kHeadDim) attn_ragged_merge_kernel(RaggedMerge
     return;
   }
   const int idx = blk - B * a.nq;
-  const int task = idx / (kPrefillRows / kMergeRows), grp = idx % (kPrefillRows / kMergeRows);
+  const int task = idx / kPrefillRows, rt = idx % kPrefillRows;  // rt: row within the tile
   const int* tp = a.header + kTaskPrefix;
   if (task >= tp[B]) return;
   int lo = 0, hi = B - 1;  // sequence of the task: largest b with tp[b] <= task
@@ -138,20 +137,27 @@ __global__ void __launch_bounds__(kHeadDim) attn_ragged_merge_kernel(RaggedMerge
   const int local = task - tp[b];
   const int tile_r = local / a.nkv, kvh = local % a.nkv;
   const int n = prefill_len(batch, b), G = a.group;
-  const int tile = prefill_tiles(n, G) - 1 - tile_r;
+  const int row = kPrefillRows * (prefill_tiles(n, G) - 1 - tile_r) + rt;
+  if (row >= n * G) return;
   const size_t unit = size_t(a.header[kUnitPrefix + b]) + size_t(tile_r * a.nkv + kvh) * parts;
   const size_t unit_floats = size_t(kPrefillRows) * (kHeadDim + 2);
-  for (int i = 0; i < kMergeRows; ++i) {
-    const int rt = kMergeRows * grp + i;  // row within the tile
-    const int row = kPrefillRows * tile + rt;
-    if (row >= n * G) break;
-    const int tok = row / G, hq = kvh * G + row % G;
-    const size_t m = size_t(batch.seq_start[b] + tok);
-    const float gt = bf16_value(a.gate[m * a.ld_gate + hq * kHeadDim + threadIdx.x]);
-    merge_row(a.prefill_partials + unit * unit_floats + size_t(rt) * (kHeadDim + 2), parts, unit_floats, gt,
-              a.out + (m * a.nq + hq) * kHeadDim, sh);
-    __syncthreads();  // sh is reused by the next row
+  const int tok = row / G, hq = kvh * G + row % G;
+  const size_t m = size_t(batch.seq_start[b] + tok);
+  const float gt = bf16_value(a.gate[m * a.ld_gate + hq * kHeadDim + threadIdx.x]);
+  // one row per workgroup, thread = dim; (m, l) of every part are read by all threads (broadcast)
+  const float* src = a.prefill_partials + unit * unit_floats + size_t(rt) * (kHeadDim + 2);
+  float M = -INFINITY;
+  for (int p = 0; p < parts; ++p) M = fmaxf(M, src[p * unit_floats + kHeadDim]);
+  float acc = 0.f, l = 0.f;
+  for (int p = 0; p < parts; ++p) {
+    const float* part = src + p * unit_floats;
+    const float mp = part[kHeadDim];
+    const float w = mp == -INFINITY ? 0.f : exp2f(mp - M);
+    l += w * part[kHeadDim + 1];
+    acc += w * part[threadIdx.x];
   }
+  const float y = (acc / l) * (1.0f / (1.0f + expf(-gt)));
+  a.out[(m * a.nq + hq) * kHeadDim + threadIdx.x] = bf16_bits(y);
 }
 
 struct RaggedShape {
@@ -210,7 +216,7 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
                        to_args(kv));
   if (int rc = check_hip(hipGetLastError(), "attention_ragged launch")) return rc;
   RaggedMergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, header, dec, pre, p.max_splits};
-  const size_t mblocks = size_t(b.num_seqs) * p.num_q_heads + s.tasks_bound * (kPrefillRows / kMergeRows);
+  const size_t mblocks = size_t(b.num_seqs) * p.num_q_heads + s.tasks_bound * kPrefillRows;
   hipLaunchKernelGGL(attn_ragged_merge_kernel, dim3(unsigned(mblocks)), dim3(kHeadDim), 0, stream, m, to_args(b));
   return check_hip(hipGetLastError(), "attention_ragged merge launch");
 }
