@@ -104,3 +104,25 @@ def test_decode_paging_permutation_bitwise():
     g1, _ = decode_step(orc, ctxs, q38a.KV_INT8, seed=6, bt_override=bt1, return_out=True)
     g2, _ = decode_step(orc, ctxs, q38a.KV_INT8, seed=6, bt_override=bt2, return_out=True)
     assert np.array_equal(g1, g2)
+
+
+def test_decode_config1_golden():
+    """Config 1 on the GPU against the reference's own golden vectors (tests/golden/config1.npz):
+    q and the appended K/V bit-exact, the output within the tolerance of the reference's bf16."""
+    from golden_util import BLOCK_TABLE, CTX, expected_pool, load, prior_pool
+    g = load()
+    pool = Pool(q38a.KV_INT8, 3, BLOCK_TABLE, fill=prior_pool(g))
+    b = Batch([(0, CTX, 1)])
+    proj_t = dev(g["proj"][None, :])
+    qn_t, kn_t = dev(g["q_norm"]), dev(g["k_norm"])
+    q_t = torch.zeros(NQ * HD, dtype=torch.int16, device="cuda")
+    out_t = torch.zeros(NQ * HD, dtype=torch.int16, device="cuda")
+    scratch_t = torch.zeros(q38a.split_scratch_floats(1, NQ, 64), dtype=torch.float32, device="cuda")
+    print("decode: config 1 golden", flush=True)
+    q38a.qk_norm_rope_append(append_params(proj_t, qn_t, kn_t, q_t, rope_dev(CTX + 1)), b.desc, pool.desc, stream())
+    q38a.attention_decode(attention_params(q_t, proj_t, out_t, scratch_t, 64), b.desc, pool.desc, stream())
+    torch.cuda.synchronize()
+    assert_bits_equal(host(q_t, np.uint16).reshape(NQ, HD), g["q16"], "q fp16")
+    assert_bits_equal(pool.download(), expected_pool(g), "pool bytes")
+    check_close(bf16_bits_to_f32(host(out_t, np.uint16))[None], bf16_bits_to_f32(g["out_bf16"])[None],
+                what="config 1 output vs reference")
