@@ -95,29 +95,37 @@ __device__ inline void split_bf16(float x, short& hi, short& lo) {
   lo = short(bf16_bits(x - bf16_value(h)));
 }
 
+// Max over the 4 rows of 16 lanes (lanes l, l ^ 16, l ^ 32, l ^ 48) with VALU lane swaps: each
+// v_permlane*_swap exchanges half of its two operands' rows, so the max of its two results is the
+// max over each pair of rows.
+__device__ inline float max_over_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+constexpr float kDecodeSlack = 8.0f;  // log2 units the running max may lag behind the true max
+
 // Online-softmax state update shared by both page formats. S holds this lane's 4 raw scores
-// (head n16, tokens 4 j4 + r); returns p[4] and rescales O when the running max moved.
+// (head n16, tokens 4 j4 + r); returns p[4] and rescales O when the running max moves. The running
+// max only moves when a block's max exceeds it by more than kDecodeSlack, so p <= 2^kDecodeSlack
+// and O is rarely rescaled after the first block.
 __device__ inline void softmax_step(const float (&S)[4], const bool (&valid)[4], float& m_run, float& l_run,
                                     float (&p)[4], float4_t (&O)[16], int j4) {
   float s2[4], bmax = -INFINITY;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    s2[r] = valid[r] ? S[r] * kScoreScale : -INFINITY;
+    s2[r] = valid[r] ? S[r] : -INFINITY;
     bmax = fmaxf(bmax, s2[r]);
   }
-  bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-  const float mnew = fmaxf(m_run, bmax);
-  const float corr = __builtin_amdgcn_exp2f(m_run - mnew);  // m_run = -inf gives 0
-  float psum = 0.f;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    p[r] = __builtin_amdgcn_exp2f(s2[r] - mnew);
-    psum += p[r];
-  }
-  l_run = l_run * corr + psum;
-  m_run = mnew;
-  if (__any(corr != 1.0f)) {
+  bmax = max_over_rows(bmax) * kScoreScale;  // kScoreScale > 0 commutes with the max
+  const bool bump = bmax > m_run + kDecodeSlack;
+  float corr = 1.0f;
+  if (__any(bump)) {
+    const float mnew = bump ? bmax : m_run;
+    corr = __builtin_amdgcn_exp2f(m_run - mnew);  // m_run = -inf gives 0
+    m_run = mnew;
     // O rows are heads 4 j4 + r; their correction factors live in lanes 4 j4 + r (quad 0)
     float cr[4];
 #pragma unroll
@@ -127,6 +135,13 @@ __device__ inline void softmax_step(const float (&S)[4], const bool (&valid)[4],
 #pragma unroll
       for (int r = 0; r < 4; ++r) O[k][r] *= cr[r];
   }
+  float psum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[r], kScoreScale, -m_run));
+    psum += p[r];
+  }
+  l_run = l_run * corr + psum;
 }
 
 // scale of (token r, group g) from a 32-byte [token][group] fp16 block
@@ -233,22 +248,25 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   // the block table is read-only during the launch: through the constant address space its
   // wave-uniform entries become scalar loads, which do not wait behind the vector loads in flight
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
-  auto load = [&](Int8Block& d, int t) {
-    const uint8_t* pg = layer + size_t(btc[t / kPageTokens]) * kv.page_bytes;
-    const int in0 = t % kPageTokens;
+  // Items start on a page boundary, so this wave's block j is token 16 * wave of page
+  // t_begin / 64 + j: only the page changes from block to block.
+  const int in0 = 16 * wave;
+  const int p0 = t_begin / kPageTokens;
+  auto load = [&](Int8Block& d, int page_id) {
+    const uint8_t* pg = layer + size_t(page_id) * kv.page_bytes;
     load_int8_block(d, pg + in0 * kHeadDim, pg + in0 * 8, off);
   };
-  auto run = [&](const Int8Block& d, int t) {
-    compute_block<true>(d, qf, t, t_end, m_run, l_run, O, j4);
-  };
-  Int8Block cur, nxt;
   const int step = 16 * kWaves;
-  int t0 = t_begin + 16 * wave;
-  if (t0 < t_end) load(cur, t0);
-  for (; t0 < t_end; t0 += step) {
-    const int t1 = t0 + step;
-    if (t1 < t_end) load(nxt, t1);
-    run(cur, t0);
+  const int t_first = t_begin + in0;
+  if (t_first >= t_end) return;
+  const int nb = (t_end - t_first + step - 1) / step;  // this wave's blocks
+  Int8Block cur, nxt;
+  load(cur, btc[p0]);
+  int pid_next = nb > 1 ? btc[p0 + 1] : 0;  // page ids are read one block ahead of their loads
+  for (int j = 0; j < nb; ++j) {
+    if (j + 1 < nb) load(nxt, pid_next);
+    pid_next = j + 2 < nb ? btc[p0 + j + 2] : 0;
+    compute_block<true>(cur, qf, t_first + j * step, t_end, m_run, l_run, O, j4);
     cur = nxt;
   }
 }
