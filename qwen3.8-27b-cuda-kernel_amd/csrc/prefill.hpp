@@ -35,11 +35,12 @@ constexpr int kRowsPerWave = 32;
 constexpr int kRowsPerTile = kPWaves * kRowsPerWave;  // 128 (token, head) rows per workgroup
 static_assert(kRowsPerTile == kPrefillRows, "prefill row tile");
 // LDS row strides (halves). K rows are read 16 B per lane by 32 different keys (528 B apart: 16
-// consecutive keys cover all banks once); V rows are read by ds_read_b64_tr_b16, four rows of 32 B
-// per 16 lanes (560 B apart: the four segments fall on distinct banks), and both are written 16 B
-// per lane by 32 consecutive keys (16-byte steps of 528 and 560 B mod 256 are all distinct).
+// consecutive keys cover all banks once). V rows are read by ds_read_b64_tr_b16, four rows of 32 B
+// per 16 lanes. Both are written 16 B per lane by 32 consecutive keys; for the V rows the stride
+// was chosen by measurement: 624 B (and 576, 608, 672) run the whole kernel ~15% faster than 560,
+// 592, 640 or 656 B, i.e. the dequantising stores are sensitive to the row stride modulo 256.
 constexpr int kKStride = kHeadDim + 8;
-constexpr int kVStride = kHeadDim + 24;
+constexpr int kVStride = kHeadDim + 56;
 constexpr float kRescaleSlack = 8.0f;
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
