@@ -7,11 +7,12 @@ namespace {
 
 // grid (tiles_x * nkv, B): block x = (tile from last to first, kv head), so the longest rows start
 // first and the kv heads of one row tile are dispatched together
+template <int DT>
 __global__ void __launch_bounds__(kPThreads, 2) attn_prefill_kernel(PrefillArgs a, BatchArgs batch, KvArgs kv) {
   __shared__ KvTile tiles[2];
   const int tiles_x = int(gridDim.x) / a.nkv;
   const int tile = tiles_x - 1 - int(blockIdx.x) / a.nkv, kvh = int(blockIdx.x) % a.nkv;
-  prefill_unit(a, batch, kv, tiles, blockIdx.y, kvh, tile, 0, 1, nullptr);
+  prefill_unit<DT>(a, batch, kv, tiles, blockIdx.y, kvh, tile, 0, 1, nullptr);
 }
 
 }  // namespace
@@ -19,12 +20,15 @@ __global__ void __launch_bounds__(kPThreads, 2) attn_prefill_kernel(PrefillArgs 
 int launch_attention_prefill(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
                              hipStream_t stream) {
   if (b.num_seqs == 0 || b.num_tokens == 0) return Q38A_OK;
-  if (kv.dtype != Q38A_KV_INT8) return set_error(Q38A_ERR_UNSUPPORTED, "attention_prefill: bf16 pages not built yet");
   const int G = p.num_q_heads / p.num_kv_heads;
   const int tiles_x = int((size_t(b.max_tokens_per_seq) * G + kRowsPerTile - 1) / kRowsPerTile);
   PrefillArgs a{p.q, p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, p.attn_layer};
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3(tiles_x * p.num_kv_heads, b.num_seqs), dim3(kPThreads), 0, stream, a,
-                     to_args(b), to_args(kv));
+  if (kv.dtype == Q38A_KV_INT8)
+    hipLaunchKernelGGL(attn_prefill_kernel<Q38A_KV_INT8>, dim3(tiles_x * p.num_kv_heads, b.num_seqs), dim3(kPThreads),
+                       0, stream, a, to_args(b), to_args(kv));
+  else
+    hipLaunchKernelGGL(attn_prefill_kernel<Q38A_KV_BF16>, dim3(tiles_x * p.num_kv_heads, b.num_seqs), dim3(kPThreads),
+                       0, stream, a, to_args(b), to_args(kv));
   return check_hip(hipGetLastError(), "attention_prefill launch");
 }
 

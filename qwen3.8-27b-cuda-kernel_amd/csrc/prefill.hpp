@@ -12,7 +12,8 @@
 //     limit is per row);
 //   * K/V tiles of 32 keys are read as int8 codes + fp16 scales with coalesced 16-byte loads one
 //     tile ahead, dequantised (code * scale, rounded once to fp16, exactly like the reference's
-//     fp16 staging) into double-buffered LDS, K and V both as [key][dim];
+//     fp16 staging) into double-buffered LDS, K and V both as [key][dim]; bf16 pages are converted
+//     to fp16 instead (exact for values in the fp16 normal range, |x| in [2^-14, 65504]);
 //   * S^T[32 keys][32 rows] = K . Q^T on v_mfma_f32_32x32x16_f16 with Q held in registers: the
 //     accumulator layout gives each lane one query row and 16 of the tile's keys, so the online
 //     softmax needs a single cross-lane step per tile;
@@ -23,6 +24,8 @@
 //     divides by l, applies sigmoid(gate) and stores bf16;
 //   * workgroups are launched last-tile-first so the longest (latest) rows start first.
 #pragma once
+
+#include <type_traits>
 
 #include "plan.hpp"
 
@@ -128,6 +131,52 @@ __device__ inline void store_tile(KvTile& T, const RawTile& R, int key0, int lim
   dequant_store32(&T.v[key][d0], R.v, live ? __builtin_bit_cast(_Float16, R.vs) : _Float16(0.0f));
 }
 
+// bf16 pages: one thread's share of a raw tile (K and V of key t % 32, dims 32 (t / 32) + [0, 32)).
+struct RawTileBf16 {
+  u32x4 k[4], v[4];
+};
+
+__device__ inline TileOffsets tile_offsets_bf16(const PageLayout& L, int kvh, int tid) {
+  TileOffsets o;
+  const int key = tid & 31, slice = tid >> 5;
+  o.k = int(L.k_row(kvh, key)) + 64 * slice;
+  o.v = int(L.v_row(kvh, key)) + 64 * slice;
+  o.ks = o.vs = 0;
+  return o;
+}
+
+// rows: page + 512 * (first key of the tile within the page)
+__device__ inline void load_raw(RawTileBf16& R, const uint8_t* rows, const uint8_t*, const TileOffsets& o) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    R.k[i] = *reinterpret_cast<const u32x4*>(rows + o.k + 16 * i);
+    R.v[i] = *reinterpret_cast<const u32x4*>(rows + o.v + 16 * i);
+  }
+}
+
+// 32 bf16 values -> fp16 at dst (exact for |x| in the fp16 normal range; zero when !live).
+__device__ inline void bf16_store32(uint16_t* dst, const u32x4 (&w)[4], bool live) {
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = w[c][i];
+      const half2_t h = {_Float16(__uint_as_float(x << 16)), _Float16(__uint_as_float(x & 0xffff0000u))};
+      o[i] = live ? __builtin_bit_cast(uint32_t, h) : 0u;
+    }
+    d[c] = o;
+  }
+}
+
+__device__ inline void store_tile(KvTile& T, const RawTileBf16& R, int key0, int limit, int tid) {
+  const int key = tid & 31, d0 = 32 * (tid >> 5);
+  const bool live = key0 + key < limit;
+  bf16_store32(&T.k[key][d0], R.k, live);
+  bf16_store32(&T.v[key][d0], R.v, live);
+}
+
 // Four consecutive keys of one dim from V [key][dim] in LDS: the lanes of each 16-lane group pass
 // the addresses of V[key0 + j / 4][dim0 + 4 (j % 4)] (j = lane % 16) and lane j receives
 // V[key0 + 0..3][dim0 + j].
@@ -142,6 +191,7 @@ __device__ inline half4_t v_keys4(const KvTile& T, int key0, int dim0, int j) {
 // of the tile's kt = ceil(kend / 32) blocks. With parts == 1 the result is final (normalised, gated,
 // bf16 into a.out); otherwise the tile's unnormalised partial goes to `partial`: [128 rows][256 + 2]
 // floats (acc[256], m, l per row in the exp2 domain, m = -inf and l = 0 for a row without keys).
+template <int DT>
 __device__ __attribute__((always_inline)) inline void prefill_unit(const PrefillArgs& a, const BatchArgs& batch,
                                                                    const KvArgs& kv, KvTile (&tiles)[2], int b,
                                                                    int kvh, int tile, int part, int parts,
@@ -189,14 +239,16 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 
   // The next tile's raw bytes are loaded into registers while the current tile is computed from
   // LDS, then dequantised into the other LDS buffer.
-  RawTile R;
+  using Raw = std::conditional_t<DT == Q38A_KV_INT8, RawTile, RawTileBf16>;
+  constexpr int kRowBytes = DT == Q38A_KV_INT8 ? kHeadDim : 2 * kHeadDim;
+  Raw R;
   auto page_ptr = [&](int key0) { return layer + size_t(bt[key0 / kPageTokens]) * kv.page_bytes; };
-  const TileOffsets toff = tile_offsets(kv.layout, kvh, tid);
-  auto fetch = [&](RawTile& RT, int j) {
+  const TileOffsets toff = DT == Q38A_KV_INT8 ? tile_offsets(kv.layout, kvh, tid) : tile_offsets_bf16(kv.layout, kvh, tid);
+  auto fetch = [&](Raw& RT, int j) {
     if (j < je) {  // uniform
       const uint8_t* pg = page_ptr(j * kKeyTile);
       const int in_page = (j * kKeyTile) % kPageTokens;
-      load_raw(RT, pg + in_page * kHeadDim, pg + in_page * 8, toff);
+      load_raw(RT, pg + in_page * kRowBytes, pg + in_page * 8, toff);
     }
   };
   auto compute = [&](const KvTile& T, int key0) {

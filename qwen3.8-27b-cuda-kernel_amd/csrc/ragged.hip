@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(kThreads, 2)
   } sh;
   const int B = batch.num_seqs;
   if (int(blockIdx.x) < r.prefill_blocks) {
-    if constexpr (DT == Q38A_KV_INT8) {
+    {
       build_prefill_plan(batch, pa.group, pa.nkv, kPrefillTarget, kMinChunk, plan);
       const int chunk = plan.chunk_pages;
       if (blockIdx.x == 0) {  // what the merge needs: parts, unit and merge-task offsets per sequence
@@ -84,7 +84,7 @@ __global__ void __launch_bounds__(kThreads, 2)
       const int parts = parts_of(batch, b, chunk);
       const int tile_r = local / (pa.nkv * parts), rem = local % (pa.nkv * parts);
       const int tile = prefill_tiles(n, pa.group) - 1 - tile_r;
-      prefill_unit(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts, parts,
+      prefill_unit<DT>(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts, parts,
                    r.prefill_partials + size_t(u) * kPrefillRows * (kHeadDim + 2));
     }
   } else {
@@ -192,8 +192,6 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   if (b.num_seqs >= kMaxSeqs) return set_error(Q38A_ERR_INVALID, "attention_ragged: at most %d sequences", kMaxSeqs - 1);
   if (p.max_splits > kMaxMergeSplits)
     return set_error(Q38A_ERR_INVALID, "attention_ragged: max_splits %d exceeds %d", p.max_splits, kMaxMergeSplits);
-  if (kv.dtype != Q38A_KV_INT8 && b.max_tokens_per_seq > 1)
-    return set_error(Q38A_ERR_UNSUPPORTED, "attention_ragged: prefill chunks over bf16 pages not built yet");
   const int G = p.num_q_heads / p.num_kv_heads;
   const RaggedShape s = ragged_shape(b.num_seqs, b.num_tokens, b.max_tokens_per_seq, p.num_q_heads, p.num_kv_heads,
                                      p.max_splits);

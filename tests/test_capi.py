@@ -91,12 +91,11 @@ def test_ragged_scratch_size_and_refusals():
     assert q38a.ragged_scratch_floats(B, B, 1, nq, nkv, splits) == 4096 + B * nq * splits * 258
     assert q38a.ragged_scratch_floats(0, 1, 1, nq, nkv, splits) == 0
     assert q38a.ragged_scratch_floats(1, 1, 1, 24, 5, splits) == 0
-    # bf16 pages: decode rows only (refused before any device call)
+    # refused before any device call
     kv = q38a.KvCacheDesc(1, 1, 4, 10, q38a.page_bytes(1, 4), q38a.page_bytes(1, 4) * 10, 1, 4)
-    p = q38a.AttentionParams(8, 8, 14336, 8, 24, 4, 0, 8, 64)
-    with pytest.raises(q38a.Q38AError, match="bf16") as e:
-        q38a.attention_ragged(p, q38a.BatchDesc(2, 5, 4, 8, 8, 8, 8, 8), kv)
-    assert e.value.code == 2
+    with pytest.raises(q38a.Q38AError, match="sequences"):
+        q38a.attention_ragged(q38a.AttentionParams(8, 8, 14336, 8, 24, 4, 0, 8, 64),
+                              q38a.BatchDesc(1024, 1024, 1, 8, 8, 8, 8, 8), kv)
     with pytest.raises(q38a.Q38AError, match="max_splits"):
         q38a.attention_ragged(q38a.AttentionParams(8, 8, 14336, 8, 24, 4, 0, 8, 600),
                               q38a.BatchDesc(2, 2, 1, 8, 8, 8, 8, 8), kv)

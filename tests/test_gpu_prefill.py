@@ -63,9 +63,16 @@ def test_prefill_chunks_from_prefixes(orc, prefix):
     prefill_step(orc, [(prefix, 37), (prefix, 64), (prefix, 90), (prefix, 211)], seed=prefix)
 
 
-def test_prefill_ragged_batch(orc):
+@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16])
+def test_prefill_ragged_batch(orc, kv_dtype):
     """Several sequences of different lengths and prefixes in one launch, incl. a 1-token row."""
-    prefill_step(orc, [(0, 130), (500, 1), (777, 300), (64, 64), (2000, 17)], seed=21)
+    prefill_step(orc, [(0, 130), (500, 1), (777, 300), (64, 64), (2000, 17)], seed=21, kv_dtype=kv_dtype)
+
+
+def test_prefill_bf16_chunks_from_prefixes(orc):
+    """bf16 pages (staged to fp16 in LDS): chunks at the reference test's prefixes."""
+    for prefix in (0, 63, 300):
+        prefill_step(orc, [(prefix, 37), (prefix, 90), (prefix, 211)], seed=40 + prefix, kv_dtype=q38a.KV_BF16)
 
 
 def test_prefill_config3_shape(orc):

@@ -83,6 +83,12 @@ def test_ragged_only_decode_bf16(orc, kv_dtype):
     ragged_step(orc, [(c, 1) for c in (5, 640, 3000, 129)], seed=33, kv_dtype=kv_dtype)
 
 
+def test_ragged_mixed_bf16(orc):
+    """bf16 pages: chunks (split and unsplit tiles) and decode rows in one launch."""
+    ragged_step(orc, [(0, 130), (5000, 1), (777, 300), (20000, 3), (63, 1)], seed=35, kv_dtype=q38a.KV_BF16,
+                compare_split_launches=True)
+
+
 def test_ragged_long_prefix_short_chunks(orc):
     """Few rows over long prefixes: every tile is cut into many key parts (merge of up to ~100)."""
     ragged_step(orc, [(20000, 2), (33000, 7), (12345, 1)], seed=34, compare_split_launches=True)
