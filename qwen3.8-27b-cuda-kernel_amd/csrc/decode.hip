@@ -33,16 +33,16 @@ struct MergeArgs {
 
 // grid (nq, B): combine the item partials of (decode row b, q head); the split count follows from
 // the decode launch's chunk size.
-__global__ void __launch_bounds__(kHeadDim) attn_merge_kernel(MergeArgs a, BatchArgs batch) {
+__global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, BatchArgs batch) {
   __shared__ MergeShared sh;
   const int hq = blockIdx.x, b = blockIdx.y;
   const int L = decode_len(batch, b);
   if (L == 0) return;
   const int row = batch.seq_start[b];
-  const float gt = bf16_value(a.gate[size_t(row) * a.ld_gate + hq * kHeadDim + threadIdx.x]);
   const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), g_chunk_pages);
   const float* src = a.scratch + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
-  merge_row(src, splits, kHeadDim + 2, gt, a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
+  merge_row(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
+            a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
 }
 
 constexpr int kBlocksPerCu = 2;
@@ -77,7 +77,8 @@ int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_des
                        to_args(kv));
   if (int rc = check_hip(hipGetLastError(), "attention_decode launch")) return rc;
   MergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.split_scratch, p.max_splits};
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(kHeadDim), 0, stream, m, to_args(b));
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(kMergeThreads), 0, stream, m,
+                     to_args(b));
   return check_hip(hipGetLastError(), "attention merge launch");
 }
 

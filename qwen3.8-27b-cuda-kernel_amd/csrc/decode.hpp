@@ -461,59 +461,77 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
   }
 }
 
+constexpr int kMergeThreads = 64;  // one wave per merged row; lane l owns dims 4l + [0, 4)
+
 struct MergeShared {
-  float w[kMaxMergeSplits], l[kMaxMergeSplits];
-  float red[kHeadDim / 64];
+  float w[kMaxMergeSplits];
 };
 
+__device__ inline float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+__device__ inline float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
 // Combines the `splits` partials at src (split s at src + s * stride: acc[256], m, l) of one
-// (row, q head) with the log-sum-exp rule, normalises, applies sigmoid(gate) and stores bf16; 256 threads, thread = dim.
-// All splits' (m, l) are fetched at once, then each thread streams the splits with eight
-// independent loads in flight.
-__device__ inline void merge_row(const float* src, int splits, size_t stride, float gate_bf16_value,
+// (row, q head) with the log-sum-exp rule, normalises, applies sigmoid(gate) and stores bf16. One
+// wave: (m, l) of all splits are reduced across the lanes, the weights go to LDS, then each lane
+// streams its 4 dims of every split (8-byte loads, eight splits in flight).
+__device__ inline void merge_row(const float* src, int splits, size_t stride, const uint16_t* gate_row,
                                  uint16_t* out_row, MergeShared& sh) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
   float mloc = -INFINITY;
-  for (int s = tid; s < splits; s += kHeadDim) {
-    const float m = src[s * stride + kHeadDim];
-    sh.w[s] = m;
-    sh.l[s] = src[s * stride + kHeadDim + 1];
-    mloc = fmaxf(mloc, m);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off, 64));
-  if (lane == 0) sh.red[wave] = mloc;
-  __syncthreads();
-  float M = sh.red[0];
-#pragma unroll
-  for (int w = 1; w < kHeadDim / 64; ++w) M = fmaxf(M, sh.red[w]);
-  __syncthreads();
+  for (int s = lane; s < splits; s += kMergeThreads) mloc = fmaxf(mloc, src[s * stride + kHeadDim]);
+  const float M = wave_max(mloc);
   float lloc = 0.f;
-  for (int s = tid; s < splits; s += kHeadDim) {
-    const float w = sh.w[s] == -INFINITY ? 0.f : exp2f(sh.w[s] - M);
+  for (int s = lane; s < splits; s += kMergeThreads) {
+    const float m = src[s * stride + kHeadDim];
+    const float w = m == -INFINITY ? 0.f : exp2f(m - M);
     sh.w[s] = w;
-    lloc += w * sh.l[s];
+    lloc += w * src[s * stride + kHeadDim + 1];
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) lloc += __shfl_xor(lloc, off, 64);
-  if (lane == 0) sh.red[wave] = lloc;
-  __syncthreads();
-  float lsum = 0.f;
-#pragma unroll
-  for (int w = 0; w < kHeadDim / 64; ++w) lsum += sh.red[w];
-  const int d = tid;
-  float acc = 0.f;
+  const float lsum = wave_sum(lloc);
+  __syncthreads();  // one wave: makes the weights visible to every lane
+  const int d = 4 * lane;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
   int s = 0;
   for (; s + 8 <= splits; s += 8) {
-    float v[8];
+    float2 v[8][2];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[(s + u) * stride + d];
+    for (int u = 0; u < 8; ++u) {
+      v[u][0] = *reinterpret_cast<const float2*>(src + (s + u) * stride + d);
+      v[u][1] = *reinterpret_cast<const float2*>(src + (s + u) * stride + d + 2);
+    }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc += sh.w[s + u] * v[u];
+    for (int u = 0; u < 8; ++u) {
+      const float w = sh.w[s + u];
+      acc[0] += w * v[u][0].x;
+      acc[1] += w * v[u][0].y;
+      acc[2] += w * v[u][1].x;
+      acc[3] += w * v[u][1].y;
+    }
   }
-  for (; s < splits; ++s) acc += sh.w[s] * src[s * stride + d];
-  const float y = (acc / lsum) * (1.0f / (1.0f + expf(-gate_bf16_value)));
-  out_row[d] = bf16_bits(y);
+  for (; s < splits; ++s) {
+    const float w = sh.w[s];
+    const float2 v0 = *reinterpret_cast<const float2*>(src + s * stride + d);
+    const float2 v1 = *reinterpret_cast<const float2*>(src + s * stride + d + 2);
+    acc[0] += w * v0.x;
+    acc[1] += w * v0.y;
+    acc[2] += w * v1.x;
+    acc[3] += w * v1.y;
+  }
+  const uint2 g = *reinterpret_cast<const uint2*>(gate_row + d);
+  const float gv[4] = {bf16_value(uint16_t(g.x)), bf16_value(uint16_t(g.x >> 16)), bf16_value(uint16_t(g.y)),
+                       bf16_value(uint16_t(g.y >> 16))};
+  uint16_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = bf16_bits((acc[i] / lsum) * (1.0f / (1.0f + expf(-gv[i]))));
+  *reinterpret_cast<uint2*>(out_row + d) = uint2{uint32_t(o[0]) | (uint32_t(o[1]) << 16), uint32_t(o[2]) | (uint32_t(o[3]) << 16)};
 }
 
 }  // namespace

@@ -106,8 +106,9 @@ struct RaggedMergeArgs {
   int max_splits;
 };
 
-// grid: B * nq decode blocks, then one block per row of every possible merge task (kPrefillRows).
-__global__ void __launch_bounds__(kHeadDim) attn_ragged_merge_kernel(RaggedMergeArgs a, BatchArgs batch) {
+// grid: B * nq decode blocks, then one block per row of every possible merge task (kPrefillRows);
+// one wave each.
+__global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(RaggedMergeArgs a, BatchArgs batch) {
   __shared__ MergeShared sh;
   const int B = batch.num_seqs;
   const int blk = blockIdx.x;
@@ -116,10 +117,10 @@ __global__ void __launch_bounds__(kHeadDim) attn_ragged_merge_kernel(RaggedMerge
     const int L = decode_len(batch, b);
     if (L == 0) return;
     const int row = batch.seq_start[b];
-    const float gt = bf16_value(a.gate[size_t(row) * a.ld_gate + hq * kHeadDim + threadIdx.x]);
     const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), a.header[0]);
     const float* src = a.decode_partials + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
-    merge_row(src, splits, kHeadDim + 2, gt, a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
+    merge_row(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
+              a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
     return;
   }
   const int idx = blk - B * a.nq;
@@ -143,21 +144,8 @@ __global__ void __launch_bounds__(kHeadDim) attn_ragged_merge_kernel(RaggedMerge
   const size_t unit_floats = size_t(kPrefillRows) * (kHeadDim + 2);
   const int tok = row / G, hq = kvh * G + row % G;
   const size_t m = size_t(batch.seq_start[b] + tok);
-  const float gt = bf16_value(a.gate[m * a.ld_gate + hq * kHeadDim + threadIdx.x]);
-  // one row per workgroup, thread = dim; (m, l) of every part are read by all threads (broadcast)
-  const float* src = a.prefill_partials + unit * unit_floats + size_t(rt) * (kHeadDim + 2);
-  float M = -INFINITY;
-  for (int p = 0; p < parts; ++p) M = fmaxf(M, src[p * unit_floats + kHeadDim]);
-  float acc = 0.f, l = 0.f;
-  for (int p = 0; p < parts; ++p) {
-    const float* part = src + p * unit_floats;
-    const float mp = part[kHeadDim];
-    const float w = mp == -INFINITY ? 0.f : exp2f(mp - M);
-    l += w * part[kHeadDim + 1];
-    acc += w * part[threadIdx.x];
-  }
-  const float y = (acc / l) * (1.0f / (1.0f + expf(-gt)));
-  a.out[(m * a.nq + hq) * kHeadDim + threadIdx.x] = bf16_bits(y);
+  merge_row(a.prefill_partials + unit * unit_floats + size_t(rt) * (kHeadDim + 2), parts, unit_floats,
+            a.gate + m * a.ld_gate + hq * kHeadDim, a.out + (m * a.nq + hq) * kHeadDim, sh);
 }
 
 struct RaggedShape {
@@ -215,7 +203,8 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   if (int rc = check_hip(hipGetLastError(), "attention_ragged launch")) return rc;
   RaggedMergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, header, dec, pre, p.max_splits};
   const size_t mblocks = size_t(b.num_seqs) * p.num_q_heads + s.tasks_bound * kPrefillRows;
-  hipLaunchKernelGGL(attn_ragged_merge_kernel, dim3(unsigned(mblocks)), dim3(kHeadDim), 0, stream, m, to_args(b));
+  hipLaunchKernelGGL(attn_ragged_merge_kernel, dim3(unsigned(mblocks)), dim3(kMergeThreads), 0, stream, m,
+                     to_args(b));
   return check_hip(hipGetLastError(), "attention_ragged merge launch");
 }
 
