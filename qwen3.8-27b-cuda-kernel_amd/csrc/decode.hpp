@@ -230,19 +230,12 @@ __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][
 // int8 pages: keys [t_begin, t_end); wave w takes the 16-token blocks t_begin + 16 (w + 4k) and
 // keeps the next block's loads in flight while it computes the current one. Block indices, pages and block-table reads are wave-uniform; only the item's last block
 // is masked.
-__device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, const uint16_t* qs,
-                                 int t_begin, int t_end, float& m_run, float& l_run, float4_t (&O)[16]) {
+__device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, int q_row,
+                                 uint16_t (*qs)[kQStride], int t_begin, int t_end, float& m_run, float& l_run,
+                                 float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, j4 = lane >> 4;
-  // Q^T operand rows in LDS (zero rows past the group): lane (head n16, k-group j4) reads dims
-  // 64g + 16 j4 + 8h + [0, 8) for group g, half h
-  const uint16_t* qlane = qs + n16 * kQStride + 16 * j4;
-  half8_t qf[4][2];
-#pragma unroll
-  for (int g = 0; g < 4; ++g)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) qf[g][h] = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
   const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
   const Int8Offsets off = int8_offsets(kv.layout, kvh, n16, j4);
   // the block table is read-only during the launch: through the constant address space its
@@ -258,11 +251,33 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   };
   const int step = 16 * kWaves;
   const int t_first = t_begin + in0;
-  if (t_first >= t_end) return;
-  const int nb = (t_end - t_first + step - 1) / step;  // this wave's blocks
+  const int nb = t_first < t_end ? (t_end - t_first + step - 1) / step : 0;  // this wave's blocks
+  // The first block's loads go out before the item's q rows are staged, so their latency overlaps
+  // the staging (every wave takes part in the staging barrier, with or without blocks).
   Int8Block cur, nxt;
-  load(cur, btc[p0]);
+  if (nb > 0) load(cur, btc[p0]);
   int pid_next = nb > 1 ? btc[p0 + 1] : 0;  // page ids are read one block ahead of their loads
+  for (int c = threadIdx.x; c < a.group * (kHeadDim / 8); c += kThreads) {
+    const int h = c / (kHeadDim / 8), c8 = (c % (kHeadDim / 8)) * 8;
+    *reinterpret_cast<u32x4*>(&qs[h][c8]) =
+        *reinterpret_cast<const u32x4*>(a.q + (size_t(q_row) * a.nq + kvh * a.group + h) * kHeadDim + c8);
+  }
+  __syncthreads();
+  if (nb == 0) return;
+  // Q^T operand (rows past the group read as zero): lane (head n16, k-group j4) holds dims
+  // 64g + 16 j4 + 8h + [0, 8) for group g, half h
+  half8_t qf[4][2];
+  {
+    const uint16_t* qlane = &qs[n16 < a.group ? n16 : 0][16 * j4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half8_t x = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
+        if (n16 >= a.group) x = half8_t{};
+        qf[g][h] = x;
+      }
+  }
   for (int j = 0; j < nb; ++j) {
     if (j + 1 < nb) load(nxt, pid_next);
     pid_next = j + 2 < nb ? btc[p0 + j + 2] : 0;
@@ -374,7 +389,7 @@ struct WaveMerge {
 };
 
 struct alignas(16) DecodeShared {
-  uint16_t q[16][kQStride];  // the item's q rows (fp16), rows past the group zero
+  uint16_t q[kMaxGroup][kQStride];  // the item's q rows (fp16)
   WaveMerge merge;           // the 4 waves' state at the end of an item
 };
 
@@ -445,15 +460,8 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
 #pragma unroll
     for (int k = 0; k < 16; ++k) O[k] = float4_t{0.f, 0.f, 0.f, 0.f};
     if constexpr (DT == Q38A_KV_INT8) {
-      // stage the item's q rows (the previous item's last barrier protects the buffer)
-      for (int c = threadIdx.x; c < 16 * (kHeadDim / 8); c += kThreads) {
-        const int h = c / (kHeadDim / 8), c8 = (c % (kHeadDim / 8)) * 8;
-        u32x4 w = u32x4{0u, 0u, 0u, 0u};
-        if (h < a.group) w = *reinterpret_cast<const u32x4*>(a.q + (size_t(q_row) * a.nq + kvh * a.group + h) * kHeadDim + c8);
-        *reinterpret_cast<u32x4*>(&sh.q[h][c8]) = w;
-      }
-      __syncthreads();
-      decode_item_int8(a, kv, bt, kvh, &sh.q[0][0], t_begin, t_end, m_run, l_run, O);
+      // stages the item's q rows itself (the previous item's last barrier protects the buffer)
+      decode_item_int8(a, kv, bt, kvh, q_row, sh.q, t_begin, t_end, m_run, l_run, O);
     } else {
       decode_item_bf16(a, kv, bt, kvh, q_row, t_begin, t_end, m_run, l_run, O);
     }
