@@ -10,7 +10,9 @@ step time, with all inputs resident in HBM. The KV pool is rotated among three c
 
 Also reported (in "extra"): the long-context decode configs 5a/5b/5c, the chunked prefill of
 config 3 (separate prefill launch and through the ragged launch) and the mixed continuous-batching
-step of config 4 (one 512-token chunk + 7 decode rows in one ragged launch; tokens/s = 519 / step).
+step of config 4 (one 512-token chunk + 7 decode rows in one ragged launch; tokens/s = 519 / step),
+and config 2 across all 16 attention layers through the native runner, as one replayed hipGraph
+per step and as eager launches.
 
 The CPU baseline is the reference's own ops.cpp attention (built from the reference sources into
 oracle/_ref, single-threaded, one token at a time in double precision) on the same contexts.
@@ -142,6 +144,64 @@ def ragged_config(name, seqs, steps, warmup, pools=3):
             "tokens_per_s": round(rb.M / (ms * 1e-3), 1), "attn_ms": round(attn_ms, 5),
             "prefill_flops": fl, "decode_kv_bytes": kvb, "t_roof_ms": round(t_roof * 1e3, 5),
             "roof_frac": round(t_roof / (attn_ms * 1e-3), 4)}
+
+
+def runner_decode_config(steps, warmup, layers=16):
+    """Config 2's decode step across all 16 full-attention layers through the native runner
+    (include/q38a_runtime.h): one hipGraph per batch bucket (metadata upload + append + decode +
+    merge for every layer, 48 kernels), replayed, against the same step launched eagerly. The KV
+    of 16 layers (3.2 GB) is far larger than the 256 MB MALL."""
+    import torch
+    import q38a
+    from q38a.runtime import Runner
+    from q38a.workloads import INT8_TOKEN_BYTES, LD, decode_contexts
+    ctxs = decode_contexts("decode_b8")
+    pages = sum((c + 1 + 63) // 64 for c in ctxs)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    qn = (1.0 + 0.1 * torch.randn(layers * 256, generator=gen, device="cuda")).float()
+    kn = (1.0 + 0.1 * torch.randn(layers * 256, generator=gen, device="cuda")).float()
+    r = Runner(qn.data_ptr(), kn.data_ptr(), kv_dtype=q38a.KV_INT8, attn_layers=layers, num_pages=pages + 8,
+               max_batch=8, max_chunk=64, max_context=32832, max_splits=256, use_graphs=True)
+    for slot, c in enumerate(ctxs):
+        assert r.ensure(slot, c + 1)
+    # random pool bytes and projection rows (synthetic): the pool through its device address
+    d = r.kv_desc()
+    pool = torch.empty(d.layer_stride * layers, dtype=torch.uint8, device="cuda")
+    pool.random_(0, 256, generator=gen)
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    # int8 codes are any byte; scales must be finite fp16: write N(0,1)/127-sized scales
+    view = pool.view(layers * d.num_pages, d.page_bytes)
+    sc = (torch.rand((layers * d.num_pages, 2 * 4 * 64 * 4), generator=gen, device="cuda") * 0.02 + 0.005)
+    view[:, 2 * 4 * 64 * 256:] = sc.to(torch.float16).view(torch.uint8).reshape(layers * d.num_pages, -1)
+    torch.cuda.synchronize()
+    assert hip.hipMemcpy(d.pool, pool.data_ptr(), pool.numel(), 4) == 0
+    b = r.buffers
+    proj = torch.randn((layers, b.rows, LD), generator=gen, device="cuda").to(torch.bfloat16)
+    assert hip.hipMemcpy(b.proj, proj.data_ptr(), proj.numel() * 2, 4) == 0
+    del pool, proj
+    s = torch.cuda.current_stream().cuda_stream
+    rows = [(slot, c) for slot, c in enumerate(ctxs)]
+    out = {}
+    for mode in ("graph", "eager"):
+        r.set_graphs(mode == "graph")
+        for _ in range(warmup):
+            r.decode(rows, s)
+        torch.cuda.synchronize()
+        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            r.decode(rows, s)
+        e.record()
+        torch.cuda.synchronize()
+        out[mode] = a.elapsed_time(e) / steps
+    kv = layers * sum(c + 1 for c in ctxs) * INT8_TOKEN_BYTES
+    r.close()
+    return {"config": "decode_b8_16_layers_runner", "layers": layers, "graph_ms": round(out["graph"], 5),
+            "eager_ms": round(out["eager"], 5), "kv_bytes": kv,
+            "graph_kv_gbs": round(kv / (out["graph"] * 1e-3) / 1e9, 1),
+            "graph_tokens_per_s": round(8 / (out["graph"] * 1e-3), 1)}
 
 
 def profile_workload(name, reps=20):
@@ -352,6 +412,8 @@ def main():
     if not only or "mixed" in only:
         from q38a.workloads import mixed_seqs
         extra["mixed_512_plus_7"] = ragged_config("mixed_512_plus_7", mixed_seqs(0), max(10, args.steps // 2), 3)
+    if not only or "runner" in only:
+        extra["decode_b8_16_layers_runner"] = runner_decode_config(max(10, args.steps // 5), 3)
     if not only or "prefill_ragged" in only:
         extra["prefill_2048_on_6000_ragged"] = ragged_config("prefill_2048_on_6000_ragged", [(6000, 2048)],
                                                              max(10, args.steps // 5), 3, pools=1)
