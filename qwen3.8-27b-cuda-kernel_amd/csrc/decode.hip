@@ -15,11 +15,10 @@ __device__ int g_chunk_pages;
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads, 2) attn_decode_kernel(DecodeArgs a, BatchArgs batch, KvArgs kv) {
-  __shared__ PlanShared plan;
   __shared__ DecodeShared sh;
-  build_plan(batch, a.nkv, a.max_splits, a.target_items, plan);
-  if (blockIdx.x == 0 && threadIdx.x == 0) g_chunk_pages = plan.chunk_pages;
-  decode_items<DT>(a, batch, kv, plan, sh, blockIdx.x, gridDim.x);
+  const DecodePlan pl = wave_decode_plan(batch, a.nkv, a.max_splits, a.target_items);
+  if (blockIdx.x == 0 && threadIdx.x == 0) g_chunk_pages = pl.cp;
+  decode_items<DT>(a, batch, kv, pl, sh, blockIdx.x, gridDim.x);
 }
 
 struct MergeArgs {
@@ -41,8 +40,8 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, 
   const int row = batch.seq_start[b];
   const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), g_chunk_pages);
   const float* src = a.scratch + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
-  merge_row(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
-            a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
+  merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
+               a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
 }
 
 constexpr int kBlocksPerCu = 2;

@@ -35,7 +35,6 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxGroup = 8;
-constexpr int kQStride = kHeadDim + 8;  // LDS row stride of q (halves): rows land on distinct banks
 constexpr int kMaxMergeSplits = 512;  // max_splits accepted by the launchers
 
 struct DecodeArgs {
@@ -125,15 +124,18 @@ __device__ inline void softmax_step(const float (&S)[4], const bool (&valid)[4],
   if (__any(bump)) {
     const float mnew = bump ? bmax : m_run;
     corr = __builtin_amdgcn_exp2f(m_run - mnew);  // m_run = -inf gives 0
+    const bool empty = m_run == -INFINITY;       // nothing accumulated yet: O rows are zero
     m_run = mnew;
-    // O rows are heads 4 j4 + r; their correction factors live in lanes 4 j4 + r (quad 0)
-    float cr[4];
+    if (!__all(empty)) {
+      // O rows are heads 4 j4 + r; their correction factors live in lanes 4 j4 + r (quad 0)
+      float cr[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * j4 + r, 64);
+      for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * j4 + r, 64);
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
+      for (int k = 0; k < 16; ++k)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) O[k][r] *= cr[r];
+        for (int r = 0; r < 4; ++r) O[k][r] *= cr[r];
+    }
   }
   float psum = 0.f;
 #pragma unroll
@@ -228,14 +230,34 @@ __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][
 }
 
 // int8 pages: keys [t_begin, t_end); wave w takes the 16-token blocks t_begin + 16 (w + 4k) and
-// keeps the next block's loads in flight while it computes the current one. Block indices, pages and block-table reads are wave-uniform; only the item's last block
-// is masked.
+// keeps the next block's loads in flight while it computes the current one. Block indices, pages and
+// block-table reads are wave-uniform; only the item's last block is masked. The waves of a
+// workgroup do not synchronise here: each loads its q operand straight from global memory.
 __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, int q_row,
-                                 uint16_t (*qs)[kQStride], int t_begin, int t_end, float& m_run, float& l_run,
-                                 float4_t (&O)[16]) {
+                                 int t_begin, int t_end, float& m_run, float& l_run, float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, j4 = lane >> 4;
+  const int step = 16 * kWaves;
+  const int in0 = 16 * wave;
+  const int t_first = t_begin + in0;
+  const int nb = t_first < t_end ? (t_end - t_first + step - 1) / step : 0;  // this wave's blocks
+  if (nb == 0) return;
+  // Q^T operand (rows past the group are zero): lane (head n16, k-group j4) holds dims
+  // 64g + 16 j4 + 8h + [0, 8) for group g, half h. Issued before the K/V loads, so waiting for it
+  // does not wait for them.
+  half8_t qf[4][2];
+  {
+    const bool real = n16 < a.group;
+    const uint16_t* qlane = a.q + (size_t(q_row) * a.nq + kvh * a.group + (real ? n16 : 0)) * kHeadDim + 16 * j4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half8_t x = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
+        qf[g][h] = real ? x : half8_t{};
+      }
+  }
   const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
   const Int8Offsets off = int8_offsets(kv.layout, kvh, n16, j4);
   // the block table is read-only during the launch: through the constant address space its
@@ -243,41 +265,14 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
   // Items start on a page boundary, so this wave's block j is token 16 * wave of page
   // t_begin / 64 + j: only the page changes from block to block.
-  const int in0 = 16 * wave;
   const int p0 = t_begin / kPageTokens;
   auto load = [&](Int8Block& d, int page_id) {
     const uint8_t* pg = layer + size_t(page_id) * kv.page_bytes;
     load_int8_block(d, pg + in0 * kHeadDim, pg + in0 * 8, off);
   };
-  const int step = 16 * kWaves;
-  const int t_first = t_begin + in0;
-  const int nb = t_first < t_end ? (t_end - t_first + step - 1) / step : 0;  // this wave's blocks
-  // The first block's loads go out before the item's q rows are staged, so their latency overlaps
-  // the staging (every wave takes part in the staging barrier, with or without blocks).
   Int8Block cur, nxt;
-  if (nb > 0) load(cur, btc[p0]);
+  load(cur, btc[p0]);
   int pid_next = nb > 1 ? btc[p0 + 1] : 0;  // page ids are read one block ahead of their loads
-  for (int c = threadIdx.x; c < a.group * (kHeadDim / 8); c += kThreads) {
-    const int h = c / (kHeadDim / 8), c8 = (c % (kHeadDim / 8)) * 8;
-    *reinterpret_cast<u32x4*>(&qs[h][c8]) =
-        *reinterpret_cast<const u32x4*>(a.q + (size_t(q_row) * a.nq + kvh * a.group + h) * kHeadDim + c8);
-  }
-  __syncthreads();
-  if (nb == 0) return;
-  // Q^T operand (rows past the group read as zero): lane (head n16, k-group j4) holds dims
-  // 64g + 16 j4 + 8h + [0, 8) for group g, half h
-  half8_t qf[4][2];
-  {
-    const uint16_t* qlane = &qs[n16 < a.group ? n16 : 0][16 * j4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        half8_t x = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
-        if (n16 >= a.group) x = half8_t{};
-        qf[g][h] = x;
-      }
-  }
   for (int j = 0; j < nb; ++j) {
     if (j + 1 < nb) load(nxt, pid_next);
     pid_next = j + 2 < nb ? btc[p0 + j + 2] : 0;
@@ -375,22 +370,23 @@ __device__ void decode_item_bf16(const DecodeArgs& a, const KvArgs& kv, const in
   }
 }
 
-// Dim of accumulator tile k, column n (depends on how V rows were mapped onto MFMA columns).
+// First of the 4 consecutive dims held by accumulator tiles 4 k4 .. 4 k4 + 3 in column n (depends on
+// how V rows were mapped onto MFMA columns): tile k, column n holds dim 64 (k / 4) + 4 n + k % 4 for
+// int8 pages and dim 16 n + k for bf16 pages.
 template <int DT>
-__device__ inline int tile_dim(int k, int n) {
-  if constexpr (DT == Q38A_KV_INT8) return 64 * (k >> 2) + 4 * n + (k & 3);
-  else return 16 * n + k;
+__device__ inline int tile_dim4(int k4, int n) {
+  if constexpr (DT == Q38A_KV_INT8) return 64 * k4 + 4 * n;
+  else return 16 * n + 4 * k4;
 }
 
-struct WaveMerge {
+struct alignas(16) WaveMerge {
+  float o[kWaves][kMaxGroup][kHeadDim];
   float m[kWaves][kMaxGroup];
   float l[kWaves][kMaxGroup];
-  float o[kWaves][kMaxGroup][kHeadDim];
 };
 
 struct alignas(16) DecodeShared {
-  uint16_t q[kMaxGroup][kQStride];  // the item's q rows (fp16)
-  WaveMerge merge;           // the 4 waves' state at the end of an item
+  WaveMerge merge;  // the 4 waves' state at the end of an item
 };
 
 // Merges the 4 waves' (m, l, O) of an item in LDS and writes the item's partial to scratch.
@@ -411,7 +407,9 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge& sm, int b, int kvh, 
     const int head = 4 * j4 + r;
     if (head < G) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) sm.o[wave][head][tile_dim<DT>(k, n16)] = O[k][r];
+      for (int k4 = 0; k4 < 4; ++k4)
+        *reinterpret_cast<float4_t*>(&sm.o[wave][head][tile_dim4<DT>(k4, n16)]) =
+            float4_t{O[4 * k4][r], O[4 * k4 + 1][r], O[4 * k4 + 2][r], O[4 * k4 + 3][r]};
     }
   }
   __syncthreads();
@@ -438,18 +436,17 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge& sm, int b, int kvh, 
 }
 
 // Persistent loop over the decode items of a launch: this workgroup is number `wg` of `nwg` that
-// stride over items; `plan` must hold build_plan's result. Partials go to a.scratch.
+// stride over items of pl.cp pages (wave_decode_plan). Partials go to a.scratch.
 template <int DT>
 __device__ __attribute__((always_inline)) inline void decode_items(const DecodeArgs& a, const BatchArgs& batch,
-                                                                   const KvArgs& kv, const PlanShared& plan,
+                                                                   const KvArgs& kv, const DecodePlan& pl,
                                                                    DecodeShared& sh, int wg, int nwg) {
-  const int B = batch.num_seqs;
-  const int total = __builtin_amdgcn_readfirstlane(plan.prefix[B]);
-  const int cp = __builtin_amdgcn_readfirstlane(plan.chunk_pages);
-  for (int item = wg; item < total; item += nwg) {
-    const int b = __builtin_amdgcn_readfirstlane(find_seq(plan, B, item));  // LDS-derived, but uniform
-    const int local = item - __builtin_amdgcn_readfirstlane(plan.prefix[b]);
-    const int split = local / a.nkv, kvh = local % a.nkv;
+  const int cp = pl.cp;
+  for (int item = wg;; item += nwg) {
+    const ItemSpot at = wave_locate(batch, a.nkv, pl, item);
+    if (at.seq < 0) break;
+    const int b = at.seq;
+    const int split = at.local / a.nkv, kvh = at.local % a.nkv;
     const int L = decode_len(batch, b);
     const int t_begin = split * cp * kPageTokens;
     const int t_end = min(L, t_begin + cp * kPageTokens);
@@ -460,8 +457,7 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
 #pragma unroll
     for (int k = 0; k < 16; ++k) O[k] = float4_t{0.f, 0.f, 0.f, 0.f};
     if constexpr (DT == Q38A_KV_INT8) {
-      // stages the item's q rows itself (the previous item's last barrier protects the buffer)
-      decode_item_int8(a, kv, bt, kvh, q_row, sh.q, t_begin, t_end, m_run, l_run, O);
+      decode_item_int8(a, kv, bt, kvh, q_row, t_begin, t_end, m_run, l_run, O);
     } else {
       decode_item_bf16(a, kv, bt, kvh, q_row, t_begin, t_end, m_run, l_run, O);
     }
@@ -469,11 +465,9 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
   }
 }
 
-constexpr int kMergeThreads = 64;  // one wave per merged row; lane l owns dims 4l + [0, 4)
-
-struct MergeShared {
-  float w[kMaxMergeSplits];
-};
+constexpr int kMergeWaves = 4;
+constexpr int kMergeThreads = 64 * kMergeWaves;
+constexpr int kMergeBatch = 16;  // splits a lane loads at once
 
 __device__ inline float wave_max(float x) {
 #pragma unroll
@@ -486,60 +480,91 @@ __device__ inline float wave_sum(float x) {
   return x;
 }
 
-// Combines the `splits` partials at src (split s at src + s * stride: acc[256], m, l) of one
-// (row, q head) with the log-sum-exp rule, normalises, applies sigmoid(gate) and stores bf16. One
-// wave: (m, l) of all splits are reduced across the lanes, the weights go to LDS, then each lane
-// streams its 4 dims of every split (8-byte loads, eight splits in flight).
-__device__ inline void merge_row(const float* src, int splits, size_t stride, const uint16_t* gate_row,
-                                 uint16_t* out_row, MergeShared& sh) {
-  const int lane = threadIdx.x & 63;
-  float mloc = -INFINITY;
-  for (int s = lane; s < splits; s += kMergeThreads) mloc = fmaxf(mloc, src[s * stride + kHeadDim]);
-  const float M = wave_max(mloc);
-  float lloc = 0.f;
-  for (int s = lane; s < splits; s += kMergeThreads) {
-    const float m = src[s * stride + kHeadDim];
-    const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-    sh.w[s] = w;
-    lloc += w * src[s * stride + kHeadDim + 1];
-  }
-  const float lsum = wave_sum(lloc);
-  __syncthreads();  // one wave: makes the weights visible to every lane
-  const int d = 4 * lane;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  int s = 0;
-  for (; s + 8 <= splits; s += 8) {
-    float2 v[8][2];
+__device__ inline float sigmoid_gate(uint16_t g) { return 1.0f / (1.0f + expf(-bf16_value(g))); }
+
+// Folds the splits s = first, first + step, ... (< splits) of one (row, q head) into a running
+// log-sum-exp state (M, lsum, acc[4] of dims d..d+3), kMergeBatch splits in flight per lane.
+// Split s sits at src + s * stride: acc[256], m, l; m = -inf marks an empty split.
+__device__ inline void fold_splits(const float* src, int first, int step, int splits, size_t stride, int d, float& M,
+                                   float& lsum, float (&acc)[4]) {
+  for (int s0 = first; s0 < splits; s0 += step * kMergeBatch) {
+    float2 v[kMergeBatch][2], ml[kMergeBatch];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      v[u][0] = *reinterpret_cast<const float2*>(src + (s + u) * stride + d);
-      v[u][1] = *reinterpret_cast<const float2*>(src + (s + u) * stride + d + 2);
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const int s = min(s0 + step * u, splits - 1);
+      const float* p = src + s * stride;
+      v[u][0] = *reinterpret_cast<const float2*>(p + d);
+      v[u][1] = *reinterpret_cast<const float2*>(p + d + 2);
+      ml[u] = *reinterpret_cast<const float2*>(p + kHeadDim);
+      if (s0 + step * u >= splits) ml[u].x = -INFINITY;
     }
+    float bm = M;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float w = sh.w[s + u];
+    for (int u = 0; u < kMergeBatch; ++u) bm = fmaxf(bm, ml[u].x);
+    if (bm == -INFINITY) continue;  // uniform: (m, l) are the same in every lane
+    const float c = __builtin_amdgcn_exp2f(M - bm);  // M = -inf gives 0
+    M = bm;
+    lsum *= c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= c;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const float w = __builtin_amdgcn_exp2f(ml[u].x - M);  // empty split: 0
+      lsum += w * ml[u].y;
       acc[0] += w * v[u][0].x;
       acc[1] += w * v[u][0].y;
       acc[2] += w * v[u][1].x;
       acc[3] += w * v[u][1].y;
     }
   }
-  for (; s < splits; ++s) {
-    const float w = sh.w[s];
-    const float2 v0 = *reinterpret_cast<const float2*>(src + s * stride + d);
-    const float2 v1 = *reinterpret_cast<const float2*>(src + s * stride + d + 2);
-    acc[0] += w * v0.x;
-    acc[1] += w * v0.y;
-    acc[2] += w * v1.x;
-    acc[3] += w * v1.y;
-  }
+}
+
+// One wave merges one (row, q head): lane l owns dims 4l + [0, 4). Used for rows with few splits.
+__device__ inline void merge_row(const float* src, int splits, size_t stride, const uint16_t* gate_row,
+                                 uint16_t* out_row) {
+  const int d = 4 * (threadIdx.x & 63);
+  float M = -INFINITY, lsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+  fold_splits(src, 0, 1, splits, stride, d, M, lsum, acc);
   const uint2 g = *reinterpret_cast<const uint2*>(gate_row + d);
-  const float gv[4] = {bf16_value(uint16_t(g.x)), bf16_value(uint16_t(g.x >> 16)), bf16_value(uint16_t(g.y)),
-                       bf16_value(uint16_t(g.y >> 16))};
+  const uint16_t gv[4] = {uint16_t(g.x), uint16_t(g.x >> 16), uint16_t(g.y), uint16_t(g.y >> 16)};
   uint16_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = bf16_bits((acc[i] / lsum) * (1.0f / (1.0f + expf(-gv[i]))));
+  for (int i = 0; i < 4; ++i) o[i] = bf16_bits((acc[i] / lsum) * sigmoid_gate(gv[i]));
   *reinterpret_cast<uint2*>(out_row + d) = uint2{uint32_t(o[0]) | (uint32_t(o[1]) << 16), uint32_t(o[2]) | (uint32_t(o[3]) << 16)};
+}
+
+struct alignas(16) MergeShared {
+  float m[kMergeWaves], l[kMergeWaves];
+  float acc[kMergeWaves][kHeadDim];
+};
+
+// The whole workgroup (kMergeWaves waves) merges one (row, q head): wave w folds splits w, w + 4,
+// ..., the waves' states are combined in LDS, and thread t finishes dim t: (acc / l) * sigmoid(gate),
+// stored as bf16 (reference attention_decode.cu:241-257).
+__device__ inline void merge_row_wg(const float* src, int splits, size_t stride, const uint16_t* gate_row,
+                                    uint16_t* out_row, MergeShared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d = 4 * lane;
+  float M = -INFINITY, lsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+  fold_splits(src, wave, kMergeWaves, splits, stride, d, M, lsum, acc);
+  if (lane == 0) {
+    sh.m[wave] = M;
+    sh.l[wave] = lsum;
+  }
+  *reinterpret_cast<float4_t*>(&sh.acc[wave][d]) = float4_t{acc[0], acc[1], acc[2], acc[3]};
+  __syncthreads();
+  const int t = threadIdx.x;
+  float Mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kMergeWaves; ++w) Mx = fmaxf(Mx, sh.m[w]);
+  float a = 0.f, l = 0.f;
+#pragma unroll
+  for (int w = 0; w < kMergeWaves; ++w) {
+    const float f = __builtin_amdgcn_exp2f(sh.m[w] - Mx);  // empty wave: 0
+    a += f * sh.acc[w][t];
+    l += f * sh.l[w];
+  }
+  out_row[t] = bf16_bits((a / l) * sigmoid_gate(gate_row[t]));
 }
 
 }  // namespace

@@ -21,11 +21,11 @@ constexpr float kScoreScale = kLog2e / 16.0f;  // 1/sqrt(256) folded into the ex
 constexpr int kMaxSeqs = 1024;  // sequences per step accepted by the attention launchers
 
 struct PlanShared {
-  int prefix[kMaxSeqs + 1];  // items before sequence b (decode rows only)
+  int prefix[kMaxSeqs + 1];  // prefill units before sequence b
   int wave_tot[kPlanThreads / 64];
   long long red_sum[kPlanThreads / 64];
   int red_max[kPlanThreads / 64];
-  int chunk_pages;  // decode plan: pages per item; prefill plan: key blocks per part
+  int chunk_pages;  // prefill plan: key blocks per part
 };
 
 // Keys of decode row b (a sequence with exactly one token in the step): [0, seq_pos0[b] + 1).
@@ -91,31 +91,80 @@ __device__ inline void block_scan_store(const int (&v)[kPlanPer], int B, int* ds
   __syncthreads();
 }
 
-// Decode plan: fills sh.prefix[0..B] (items before decode row b) and sh.chunk_pages.
-// Must be called by all kPlanThreads threads.
-__device__ inline void build_plan(const BatchArgs& batch, int nkv, int max_splits, int target_items, PlanShared& sh) {
-  const int B = batch.num_seqs;
-  int pages[kPlanPer];
-  long long psum = 0;
-  int pmax = 0;
+// Decode plan, computed by every wave on its own (no LDS, no barrier), so a workgroup's first loads
+// wait only for the sequence metadata. Sequences are scanned 64 at a time, one per lane.
+__device__ inline int wave_sum_i(int x) {
 #pragma unroll
-  for (int i = 0; i < kPlanPer; ++i) {
-    const int s = threadIdx.x * kPlanPer + i;
-    pages[i] = s < B ? ceil_div_i(decode_len(batch, s), kPageTokens) : 0;
-    psum += pages[i];
-    pmax = max(pmax, pages[i]);
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+__device__ inline int wave_max_i(int x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = max(x, __shfl_xor(x, off, 64));
+  return x;
+}
+
+struct DecodePlan {
+  int cp;      // pages per item (wave-uniform)
+  int pages0;  // pages of decode row `lane` (rows 0..63), kept so locating items rereads nothing
+};
+
+__device__ inline int decode_pages(const BatchArgs& batch, int s) {
+  return s < batch.num_seqs ? ceil_div_i(decode_len(batch, s), kPageTokens) : 0;
+}
+
+// Pages per item of a decode launch: every row needs at most max_splits items per kv head, and the
+// batch yields about target_items items.
+__device__ inline DecodePlan wave_decode_plan(const BatchArgs& batch, int nkv, int max_splits, int target_items) {
+  const int lane = threadIdx.x & 63;
+  DecodePlan pl;
+  pl.pages0 = decode_pages(batch, lane);
+  int psum = pl.pages0, pmax = pl.pages0;  // pages: < 2^31 for any pool a 32-bit block table addresses
+  for (int s0 = 64; s0 < batch.num_seqs; s0 += 64) {
+    const int p = decode_pages(batch, s0 + lane);
+    psum += p;
+    pmax = max(pmax, p);
   }
-  long long tot;
-  int mx;
-  block_sum_max(psum, pmax, sh, tot, mx);
-  const int by_splits = ceil_div_i(mx, max_splits);
-  const int by_target = int((tot * nkv + target_items - 1) / target_items);
-  const int cp = max(1, max(by_splits, by_target));
-  if (threadIdx.x == 0) sh.chunk_pages = cp;
-  int items[kPlanPer];
+  psum = wave_sum_i(psum);
+  pmax = wave_max_i(pmax);
+  const int by_splits = ceil_div_i(pmax, max_splits);
+  const int by_target = int((static_cast<long long>(psum) * nkv + target_items - 1) / target_items);
+  pl.cp = __builtin_amdgcn_readfirstlane(max(1, max(by_splits, by_target)));
+  return pl;
+}
+
+struct ItemSpot {
+  int seq;    // decode row of the item, or -1 past the last item
+  int local;  // item index within the row's items
+};
+
+// Locates decode item `item`: the items of row b are ceil(pages_b / cp) * nkv, in row order
+// (wave-uniform result).
+__device__ inline ItemSpot wave_locate(const BatchArgs& batch, int nkv, const DecodePlan& pl, int item) {
+  const int lane = threadIdx.x & 63;
+  ItemSpot r{-1, 0};
+  int base = 0;
+  for (int s0 = 0; s0 < batch.num_seqs && base <= item; s0 += 64) {
+    const int p = s0 == 0 ? pl.pages0 : decode_pages(batch, s0 + lane);
+    const int n = ceil_div_i(p, pl.cp) * nkv;
+    int incl = n;
 #pragma unroll
-  for (int i = 0; i < kPlanPer; ++i) items[i] = ceil_div_i(pages[i], cp) * nkv;
-  block_scan_store(items, B, sh.prefix, sh);
+    for (int off = 1; off < 64; off <<= 1) {
+      const int x = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += x;
+    }
+    const int excl = base + incl - n;
+    const unsigned long long hit = __ballot(n > 0 && excl <= item && item < excl + n);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      r.seq = s0 + l;
+      r.local = item - __shfl(excl, l, 64);
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  r.seq = __builtin_amdgcn_readfirstlane(r.seq);
+  r.local = __builtin_amdgcn_readfirstlane(r.local);
+  return r;
 }
 
 // ---- prefill units ------------------------------------------------------------------------------

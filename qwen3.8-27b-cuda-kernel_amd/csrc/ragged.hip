@@ -15,7 +15,7 @@
 //     chip; a tile with one part stores its final output, otherwise each part stores an
 //     unnormalised partial;
 //   * decode: the persistent split-KV loop of attention_decode over the decode rows' items;
-//   * merge: one workgroup per (decode row, q head) and one per row of each split prefill tile.
+//   * merge: one workgroup per (decode row, q head) and one wave per row of each split prefill tile.
 // The plan is recomputed on the device from seq_start / seq_pos0 (graph-capturable); the first
 // workgroup of each kind records what the merge needs in the scratch header.
 //
@@ -88,10 +88,10 @@ __global__ void __launch_bounds__(kThreads, 2)
                    r.prefill_partials + size_t(u) * kPrefillRows * (kHeadDim + 2));
     }
   } else {
-    build_plan(batch, d.nkv, d.max_splits, d.target_items, plan);
+    const DecodePlan pl = wave_decode_plan(batch, d.nkv, d.max_splits, d.target_items);
     const int wg = int(blockIdx.x) - r.prefill_blocks;
-    if (wg == 0 && threadIdx.x == 0) r.header[0] = plan.chunk_pages;
-    decode_items<DT>(d, batch, kv, plan, sh.dec, wg, int(gridDim.x) - r.prefill_blocks);
+    if (wg == 0 && threadIdx.x == 0) r.header[0] = pl.cp;
+    decode_items<DT>(d, batch, kv, pl, sh.dec, wg, int(gridDim.x) - r.prefill_blocks);
   }
 }
 
@@ -106,8 +106,8 @@ struct RaggedMergeArgs {
   int max_splits;
 };
 
-// grid: B * nq decode blocks, then one block per row of every possible merge task (kPrefillRows);
-// one wave each.
+// grid: B * nq decode blocks (a workgroup per decode row and q head), then kPrefillRows / 4 blocks
+// per possible merge task (a wave per row of the split tile).
 __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(RaggedMergeArgs a, BatchArgs batch) {
   __shared__ MergeShared sh;
   const int B = batch.num_seqs;
@@ -119,12 +119,14 @@ __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(Ragged
     const int row = batch.seq_start[b];
     const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), a.header[0]);
     const float* src = a.decode_partials + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
-    merge_row(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
-              a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
+    merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
+                 a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
     return;
   }
   const int idx = blk - B * a.nq;
-  const int task = idx / kPrefillRows, rt = idx % kPrefillRows;  // rt: row within the tile
+  constexpr int kBlocksPerTask = kPrefillRows / kMergeWaves;
+  const int task = idx / kBlocksPerTask;
+  const int rt = (idx % kBlocksPerTask) * kMergeWaves + int(threadIdx.x >> 6);  // row within the tile
   const int* tp = a.header + kTaskPrefix;
   if (task >= tp[B]) return;
   int lo = 0, hi = B - 1;  // sequence of the task: largest b with tp[b] <= task
@@ -145,7 +147,7 @@ __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(Ragged
   const int tok = row / G, hq = kvh * G + row % G;
   const size_t m = size_t(batch.seq_start[b] + tok);
   merge_row(a.prefill_partials + unit * unit_floats + size_t(rt) * (kHeadDim + 2), parts, unit_floats,
-            a.gate + m * a.ld_gate + hq * kHeadDim, a.out + (m * a.nq + hq) * kHeadDim, sh);
+            a.gate + m * a.ld_gate + hq * kHeadDim, a.out + (m * a.nq + hq) * kHeadDim);
 }
 
 struct RaggedShape {
@@ -202,7 +204,7 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
                        to_args(kv));
   if (int rc = check_hip(hipGetLastError(), "attention_ragged launch")) return rc;
   RaggedMergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, header, dec, pre, p.max_splits};
-  const size_t mblocks = size_t(b.num_seqs) * p.num_q_heads + s.tasks_bound * kPrefillRows;
+  const size_t mblocks = size_t(b.num_seqs) * p.num_q_heads + s.tasks_bound * (kPrefillRows / kMergeWaves);
   hipLaunchKernelGGL(attn_ragged_merge_kernel, dim3(unsigned(mblocks)), dim3(kMergeThreads), 0, stream, m,
                      to_args(b));
   return check_hip(hipGetLastError(), "attention_ragged merge launch");
