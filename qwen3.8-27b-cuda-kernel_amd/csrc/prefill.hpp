@@ -90,14 +90,20 @@ __device__ inline TileOffsets tile_offsets(const PageLayout& L, int kvh, int tid
   return o;
 }
 
-// rows: page + 256 * (first key of the tile within the page); sc: page + 8 * (same key)
-__device__ inline void load_raw(RawTile& R, const uint8_t* rows, const uint8_t* sc, const TileOffsets& o) {
-  R.k[0] = *reinterpret_cast<const u32x4*>(rows + o.k);
-  R.k[1] = *reinterpret_cast<const u32x4*>(rows + o.k + 16);
-  R.v[0] = *reinterpret_cast<const u32x4*>(rows + o.v);
-  R.v[1] = *reinterpret_cast<const u32x4*>(rows + o.v + 16);
-  R.ks = *reinterpret_cast<const uint16_t*>(sc + o.ks);
-  R.vs = *reinterpret_cast<const uint16_t*>(sc + o.vs);
+// A page as a buffer resource: its loads take a scalar base, this lane's 32-bit offset and a scalar
+// offset (the tile's first key), so no 64-bit per-lane addresses are kept in registers.
+__device__ inline __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* page, size_t page_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page), short(0), int(page_bytes), 0x00020000);
+}
+
+// srow: byte offset of the tile's first key row within the page; ssc: the same for its scales
+__device__ inline void load_raw(RawTile& R, __amdgpu_buffer_rsrc_t pg, int srow, int ssc, const TileOffsets& o) {
+  R.k[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.k, srow, 0));
+  R.k[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.k, srow + 16, 0));
+  R.v[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.v, srow, 0));
+  R.v[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.v, srow + 16, 0));
+  R.ks = __builtin_amdgcn_raw_buffer_load_b16(pg, o.ks, ssc, 0);
+  R.vs = __builtin_amdgcn_raw_buffer_load_b16(pg, o.vs, ssc, 0);
 }
 
 // code * scale rounded once to fp16, for a pair: the biased fp16 (1024 + c + 128) minus 1152 is the
@@ -145,12 +151,11 @@ __device__ inline TileOffsets tile_offsets_bf16(const PageLayout& L, int kvh, in
   return o;
 }
 
-// rows: page + 512 * (first key of the tile within the page)
-__device__ inline void load_raw(RawTileBf16& R, const uint8_t* rows, const uint8_t*, const TileOffsets& o) {
+__device__ inline void load_raw(RawTileBf16& R, __amdgpu_buffer_rsrc_t pg, int srow, int, const TileOffsets& o) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    R.k[i] = *reinterpret_cast<const u32x4*>(rows + o.k + 16 * i);
-    R.v[i] = *reinterpret_cast<const u32x4*>(rows + o.v + 16 * i);
+    R.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.k, srow + 16 * i, 0));
+    R.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.v, srow + 16 * i, 0));
   }
 }
 
@@ -242,13 +247,14 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
   using Raw = std::conditional_t<DT == Q38A_KV_INT8, RawTile, RawTileBf16>;
   constexpr int kRowBytes = DT == Q38A_KV_INT8 ? kHeadDim : 2 * kHeadDim;
   Raw R;
-  auto page_ptr = [&](int key0) { return layer + size_t(bt[key0 / kPageTokens]) * kv.page_bytes; };
+  // page ids through the constant address space: scalar loads, so a tile's page is a scalar base
+  const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
+  auto page_ptr = [&](int key0) { return layer + size_t(btc[key0 / kPageTokens]) * kv.page_bytes; };
   const TileOffsets toff = DT == Q38A_KV_INT8 ? tile_offsets(kv.layout, kvh, tid) : tile_offsets_bf16(kv.layout, kvh, tid);
   auto fetch = [&](Raw& RT, int j) {
     if (j < je) {  // uniform
-      const uint8_t* pg = page_ptr(j * kKeyTile);
       const int in_page = (j * kKeyTile) % kPageTokens;
-      load_raw(RT, pg + in_page * kRowBytes, pg + in_page * 8, toff);
+      load_raw(RT, page_rsrc(page_ptr(j * kKeyTile), kv.page_bytes), in_page * kRowBytes, in_page * 8, toff);
     }
   };
   auto compute = [&](const KvTile& T, int key0) {
