@@ -362,11 +362,45 @@ def cpu_baseline(batch, budget_s=20.0):
         done_bytes += L * (2112 if batch.dtype == q38a.KV_INT8 else 4096)
         if spent > budget_s:
             break
-    return {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{done_tokens} of {batch.B} decode rows (shortest first), one attention layer, "
-                      f"{done_bytes / 2112 if batch.dtype == 0 else done_bytes / 4096:.0f} KV tokens, "
-                      f"{spent:.2f} s single-threaded; tokens/s = {done_tokens / spent:.3f}",
-            "tokens_per_s": done_tokens / spent}
+    out = {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+           "sample": f"{done_tokens} of {batch.B} decode rows (shortest first), one attention layer, "
+                     f"{done_bytes / 2112 if batch.dtype == 0 else done_bytes / 4096:.0f} KV tokens, "
+                     f"{spent:.2f} s single-threaded; tokens/s = {done_tokens / spent:.3f}",
+           "tokens_per_s": done_tokens / spent}
+    # The same rows again, one thread per row on the host's cores (the reference path is serial per
+    # token; rows are independent). ctypes releases the GIL during the call.
+    rows = order[:done_tokens]
+    cores = min(len(rows), len(os.sched_getaffinity(0)))
+    if kind == "reference" and cores > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        stores = []
+        for b in rows:
+            L = batch.ctxs[b] + 1
+            k, v = orc.read_back(pool, batch.dtype, 4, batch.block_table, b, L)
+            st = ref.store(4, L)
+            st.k[...] = k
+            st.v[...] = v
+            stores.append((st, f16_to_f32(q16[b]).ravel(), bf16_to_f32(gate[b]), L - 1))
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(cores) as ex:
+            list(ex.map(lambda a: a[0].attention_token(24, a[1], a[2], a[3]), stores))
+        wall = time.perf_counter() - t0
+        for st, *_ in stores:
+            st.close()
+        out["all_cores"] = {"value": done_bytes / wall / 1e9, "cores": cores, "wall_s": round(wall, 3),
+                            "tokens_per_s": done_tokens / wall}
+    out["host"] = {"nproc": len(os.sched_getaffinity(0)), "cpu": cpu_model()}
+    return out
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():

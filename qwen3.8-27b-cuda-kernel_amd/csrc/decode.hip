@@ -25,7 +25,7 @@ struct MergeArgs {
   const uint16_t* gate;
   int ld_gate;
   uint16_t* out;
-  int nq;
+  int nq, group;
   const float* scratch;
   int max_splits;
 };
@@ -39,6 +39,7 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, 
   if (L == 0) return;
   const int row = batch.seq_start[b];
   const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), g_chunk_pages);
+  if (hq % a.group == 0) reset_claims(b, hq / a.group, splits);  // the decode launch is complete
   const float* src = a.scratch + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
   merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
                a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
@@ -75,7 +76,8 @@ int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_des
     hipLaunchKernelGGL(attn_decode_kernel<Q38A_KV_BF16>, dim3(grid), dim3(kThreads), 0, stream, a, to_args(b),
                        to_args(kv));
   if (int rc = check_hip(hipGetLastError(), "attention_decode launch")) return rc;
-  MergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.split_scratch, p.max_splits};
+  MergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_q_heads / p.num_kv_heads, p.split_scratch,
+              p.max_splits};
   hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(kMergeThreads), 0, stream, m,
                      to_args(b));
   return check_hip(hipGetLastError(), "attention merge launch");

@@ -229,20 +229,28 @@ __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][
   }
 }
 
-// int8 pages: keys [t_begin, t_end); wave w takes the 16-token blocks t_begin + 16 (w + 4k) and
-// keeps the next block's loads in flight while it computes the current one. Block indices, pages and
-// block-table reads are wave-uniform; only the item's last block is masked. The waves of a
-// workgroup do not synchronise here: each loads its q operand straight from global memory.
+// The 16-token blocks a wave works through. Static: blocks first, first + stride, ... of [tb, te).
+// Dynamic (ctr != nullptr): the wave starts with block `first`, then claims blocks from a counter
+// shared by a team of workgroups (a claim returning c means block base + c), so waves on faster CUs
+// or XCDs take more of the team's blocks and the team finishes together.
+struct BlockSource {
+  int tb, te;   // tokens [tb, te); tb is page aligned
+  int nblk;     // 16-token blocks in [tb, te)
+  int first;    // this wave's first block
+  int stride;   // static schedule step
+  int base;     // dynamic: first claimable block
+  int* ctr;     // dynamic: the team's claim counter
+};
+
+// int8 pages: the blocks of `src`; the next block's loads are in flight while the current one is
+// computed, and with a claim counter the claim after that is in flight too. Block indices, pages
+// and block-table reads are wave-uniform; blocks past te are masked. The waves of a workgroup do
+// not synchronise here: each loads its q operand straight from global memory.
 __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, int q_row,
-                                 int t_begin, int t_end, float& m_run, float& l_run, float4_t (&O)[16]) {
+                                 const BlockSource& src, float& m_run, float& l_run, float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, j4 = lane >> 4;
-  const int step = 16 * kWaves;
-  const int in0 = 16 * wave;
-  const int t_first = t_begin + in0;
-  const int nb = t_first < t_end ? (t_end - t_first + step - 1) / step : 0;  // this wave's blocks
-  if (nb == 0) return;
+  if (src.first >= src.nblk) return;
   // Q^T operand (rows past the group are zero): lane (head n16, k-group j4) holds dims
   // 64g + 16 j4 + 8h + [0, 8) for group g, half h. Issued before the K/V loads, so waiting for it
   // does not wait for them.
@@ -263,21 +271,40 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   // the block table is read-only during the launch: through the constant address space its
   // wave-uniform entries become scalar loads, which do not wait behind the vector loads in flight
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
-  // Items start on a page boundary, so this wave's block j is token 16 * wave of page
-  // t_begin / 64 + j: only the page changes from block to block.
-  const int p0 = t_begin / kPageTokens;
-  auto load = [&](Int8Block& d, int page_id) {
-    const uint8_t* pg = layer + size_t(page_id) * kv.page_bytes;
+  auto load = [&](Int8Block& d, int idx) {
+    const int t0 = src.tb + 16 * idx;
+    const uint8_t* pg = layer + size_t(btc[t0 / kPageTokens]) * kv.page_bytes;
+    const int in0 = t0 % kPageTokens;
     load_int8_block(d, pg + in0 * kHeadDim, pg + in0 * 8, off);
   };
+  // one lane claims; the value is read (readfirstlane) only when the next block is chosen
+  auto claim = [&]() {
+    int c = 0;
+    if (lane == 0) c = __hip_atomic_fetch_add(src.ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return c;
+  };
+  // Each claim is issued before the loads of the block it follows, so resolving it (a wait on the
+  // vector memory counter) never waits for K/V data: the next block's loads always go out before
+  // the current block's data is awaited.
+  const bool dynamic = src.ctr != nullptr;
+  int idx = src.first;
+  int pending = dynamic ? claim() : 0;
   Int8Block cur, nxt;
-  load(cur, btc[p0]);
-  int pid_next = nb > 1 ? btc[p0 + 1] : 0;  // page ids are read one block ahead of their loads
-  for (int j = 0; j < nb; ++j) {
-    if (j + 1 < nb) load(nxt, pid_next);
-    pid_next = j + 2 < nb ? btc[p0 + j + 2] : 0;
-    compute_block<true>(cur, qf, t_first + j * step, t_end, m_run, l_run, O, j4);
+  load(cur, idx);
+  for (;;) {
+    // the empty asm pins the claim's use here: without it the compiler reads the claim right after
+    // issuing it, which waits for every load in flight
+    if (dynamic) asm volatile("" : "+v"(pending));
+    const int nidx = dynamic ? src.base + __builtin_amdgcn_readfirstlane(pending) : idx + src.stride;
+    const bool more = nidx < src.nblk;  // uniform
+    if (more && dynamic) pending = claim();
+    // unconditional (the last iteration reloads the current block): with a single path the
+    // compiler's wait for the current block does not also cover the next block's loads
+    load(nxt, more ? nidx : idx);
+    compute_block<true>(cur, qf, src.tb + 16 * idx, src.te, m_run, l_run, O, j4);
+    if (!more) break;
     cur = nxt;
+    idx = nidx;
   }
 }
 
@@ -435,21 +462,44 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge& sm, int b, int kvh, 
   __syncthreads();
 }
 
+// Claim counters of the dynamic block schedule, one per team (decode row, kv head, team of up to
+// kTeam consecutive splits). They start at zero (static storage) and the merge launch that follows
+// a decode launch on the same stream resets the ones it used, so every launch finds them at zero.
+// Launches that overlap in time on one device would share them: run them on one stream.
+constexpr int kTeam = 8;            // workgroups (splits) per team: consecutive ones sit on 8 XCDs
+constexpr int kClaimKvHeads = 8;    // kv heads covered by the counters (more: static schedule)
+constexpr int kClaimTeams = kMaxMergeSplits / kTeam;
+__device__ int g_claims[kMaxSeqs * kClaimKvHeads * kClaimTeams];
+
+__device__ inline int* claim_counter(int b, int kvh, int team) {
+  return &g_claims[(size_t(b) * kClaimKvHeads + kvh) * kClaimTeams + team];
+}
+
+// Zeroes the counters of decode row b, kv head kvh (splits of the row: nsplit); one workgroup.
+__device__ inline void reset_claims(int b, int kvh, int nsplit) {
+  if (kvh >= kClaimKvHeads) return;
+  for (int t = threadIdx.x; t < ceil_div_i(nsplit, kTeam); t += blockDim.x) *claim_counter(b, kvh, t) = 0;
+}
+
 // Persistent loop over the decode items of a launch: this workgroup is number `wg` of `nwg` that
-// stride over items of pl.cp pages (wave_decode_plan). Partials go to a.scratch.
+// stride over items of pl.cp pages (wave_decode_plan). The items of a decode row are ordered
+// (kv head, split), so the splits of one (row, kv head) are consecutive workgroups, i.e. spread
+// over the XCDs; teams of kTeam of them share a claim counter over their pages (int8 pages).
+// Partials go to a.scratch.
 template <int DT>
 __device__ __attribute__((always_inline)) inline void decode_items(const DecodeArgs& a, const BatchArgs& batch,
                                                                    const KvArgs& kv, const DecodePlan& pl,
                                                                    DecodeShared& sh, int wg, int nwg) {
   const int cp = pl.cp;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   for (int item = wg;; item += nwg) {
     const ItemSpot at = wave_locate(batch, a.nkv, pl, item);
     if (at.seq < 0) break;
     const int b = at.seq;
-    const int split = at.local / a.nkv, kvh = at.local % a.nkv;
     const int L = decode_len(batch, b);
-    const int t_begin = split * cp * kPageTokens;
-    const int t_end = min(L, t_begin + cp * kPageTokens);
+    const int nsplit = ceil_div_i(ceil_div_i(L, kPageTokens), cp);
+    const int kvh = at.local / nsplit, split = at.local % nsplit;
+    const int span = cp * kPageTokens;  // tokens per split
     const int* bt = kv.block_table + size_t(batch.seq_slot[b]) * kv.max_pages_per_seq;
     const int q_row = batch.seq_start[b];
     float m_run = -INFINITY, l_run = 0.f;
@@ -457,9 +507,27 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
 #pragma unroll
     for (int k = 0; k < 16; ++k) O[k] = float4_t{0.f, 0.f, 0.f, 0.f};
     if constexpr (DT == Q38A_KV_INT8) {
-      decode_item_int8(a, kv, bt, kvh, q_row, t_begin, t_end, m_run, l_run, O);
+      BlockSource src;
+      const int team = split / kTeam, member = split % kTeam;
+      if (kvh < kClaimKvHeads) {
+        const int members = min(kTeam, nsplit - team * kTeam);
+        src.tb = team * kTeam * span;
+        src.te = min(L, src.tb + members * span);
+        src.first = member * kWaves + wave;
+        src.base = members * kWaves;
+        src.ctr = claim_counter(b, kvh, team);
+      } else {
+        src.tb = split * span;
+        src.te = min(L, src.tb + span);
+        src.first = wave;
+        src.ctr = nullptr;
+      }
+      src.nblk = ceil_div_i(src.te - src.tb, 16);
+      src.stride = kWaves;
+      decode_item_int8(a, kv, bt, kvh, q_row, src, m_run, l_run, O);
     } else {
-      decode_item_bf16(a, kv, bt, kvh, q_row, t_begin, t_end, m_run, l_run, O);
+      const int t_begin = split * span;
+      decode_item_bf16(a, kv, bt, kvh, q_row, t_begin, min(L, t_begin + span), m_run, l_run, O);
     }
     finish_item<DT>(a, sh.merge, b, kvh, split, m_run, l_run, O);
   }
