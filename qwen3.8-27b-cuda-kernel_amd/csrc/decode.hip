@@ -39,7 +39,6 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, 
   if (L == 0) return;
   const int row = batch.seq_start[b];
   const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), g_chunk_pages);
-  if (hq % a.group == 0) reset_claims(b, hq / a.group, splits);  // the decode launch is complete
   const float* src = a.scratch + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
   merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
                a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);

@@ -238,9 +238,17 @@ struct BlockSource {
   int nblk;     // 16-token blocks in [tb, te)
   int first;    // this wave's first block
   int stride;   // static schedule step
-  int base;     // dynamic: first claimable block
+  int base;     // dynamic: first claimable block (the team's waves start with blocks [0, base))
   int* ctr;     // dynamic: the team's claim counter
 };
+
+// A team's counter ends a launch at (successful claims) + (one failing claim per wave that had a
+// first block); the wave whose failing claim returns the last value resets it, so every launch
+// finds it at zero.
+__device__ inline bool last_claim(const BlockSource& src, int c) {
+  const int waves = min(src.base, src.nblk);
+  return c == max(0, src.nblk - src.base) + waves - 1;
+}
 
 // int8 pages: the blocks of `src`; the next block's loads are in flight while the current one is
 // computed, and with a claim counter the claim after that is in flight too. Block indices, pages
@@ -295,8 +303,11 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
     // the empty asm pins the claim's use here: without it the compiler reads the claim right after
     // issuing it, which waits for every load in flight
     if (dynamic) asm volatile("" : "+v"(pending));
-    const int nidx = dynamic ? src.base + __builtin_amdgcn_readfirstlane(pending) : idx + src.stride;
+    const int c = __builtin_amdgcn_readfirstlane(pending);
+    const int nidx = dynamic ? src.base + c : idx + src.stride;
     const bool more = nidx < src.nblk;  // uniform
+    if (dynamic && !more && last_claim(src, c) && lane == 0)
+      __hip_atomic_store(src.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (more && dynamic) pending = claim();
     // unconditional (the last iteration reloads the current block): with a single path the
     // compiler's wait for the current block does not also cover the next block's loads
@@ -462,29 +473,21 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge& sm, int b, int kvh, 
   __syncthreads();
 }
 
-// Claim counters of the dynamic block schedule, one per team (decode row, kv head, team of up to
-// kTeam consecutive splits). They start at zero (static storage) and the merge launch that follows
-// a decode launch on the same stream resets the ones it used, so every launch finds them at zero.
-// Launches that overlap in time on one device would share them: run them on one stream.
+// Claim counters of the dynamic block schedule, one per team of up to kTeam consecutive splits of
+// a (decode row, kv head), in the slot of the team's first item, one 128-byte line each (claims on
+// one line serialise). They start at zero (static storage) and the last claim of a launch resets
+// its counter (last_claim). Launches that overlap in time on one device would share them: run
+// them on one stream.
 constexpr int kTeam = 8;            // workgroups (splits) per team: consecutive ones sit on 8 XCDs
-constexpr int kClaimKvHeads = 8;    // kv heads covered by the counters (more: static schedule)
-constexpr int kClaimTeams = kMaxMergeSplits / kTeam;
-__device__ int g_claims[kMaxSeqs * kClaimKvHeads * kClaimTeams];
-
-__device__ inline int* claim_counter(int b, int kvh, int team) {
-  return &g_claims[(size_t(b) * kClaimKvHeads + kvh) * kClaimTeams + team];
-}
-
-// Zeroes the counters of decode row b, kv head kvh (splits of the row: nsplit); one workgroup.
-__device__ inline void reset_claims(int b, int kvh, int nsplit) {
-  if (kvh >= kClaimKvHeads) return;
-  for (int t = threadIdx.x; t < ceil_div_i(nsplit, kTeam); t += blockDim.x) *claim_counter(b, kvh, t) = 0;
-}
+constexpr int kClaimSlots = 4096;   // teams whose first item index is larger use the static schedule
+constexpr int kClaimStride = 32;    // ints per slot
+__device__ int g_claims[kClaimSlots * kClaimStride];
 
 // Persistent loop over the decode items of a launch: this workgroup is number `wg` of `nwg` that
 // stride over items of pl.cp pages (wave_decode_plan). The items of a decode row are ordered
 // (kv head, split), so the splits of one (row, kv head) are consecutive workgroups, i.e. spread
-// over the XCDs; teams of kTeam of them share a claim counter over their pages (int8 pages).
+// over the XCDs; teams of kTeam of them share a claim counter over their pages (int8 pages; the
+// items of one row are consecutive, so a team's items are items slot .. slot + members - 1).
 // Partials go to a.scratch.
 template <int DT>
 __device__ __attribute__((always_inline)) inline void decode_items(const DecodeArgs& a, const BatchArgs& batch,
@@ -509,13 +512,14 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
     if constexpr (DT == Q38A_KV_INT8) {
       BlockSource src;
       const int team = split / kTeam, member = split % kTeam;
-      if (kvh < kClaimKvHeads) {
+      const int slot = item - member;  // the team's first item
+      if (slot < kClaimSlots) {
         const int members = min(kTeam, nsplit - team * kTeam);
         src.tb = team * kTeam * span;
         src.te = min(L, src.tb + members * span);
         src.first = member * kWaves + wave;
         src.base = members * kWaves;
-        src.ctr = claim_counter(b, kvh, team);
+        src.ctr = &g_claims[slot * kClaimStride];
       } else {
         src.tb = split * span;
         src.te = min(L, src.tb + span);
