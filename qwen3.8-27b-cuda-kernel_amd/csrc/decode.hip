@@ -67,7 +67,7 @@ int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_des
   int grid = 0, target = 0;
   if (int rc = decode_grid(&grid, &target)) return rc;
   DecodeArgs a{p.q, p.num_q_heads, p.num_kv_heads, p.num_q_heads / p.num_kv_heads, p.attn_layer,
-               p.split_scratch, p.max_splits, target, p.gate, p.ld_gate, p.out};
+               p.split_scratch, p.max_splits, target, p.gate, p.ld_gate, p.out, false};
   if (kv.dtype == Q38A_KV_INT8)
     hipLaunchKernelGGL(attn_decode_kernel<Q38A_KV_INT8>, dim3(grid), dim3(kThreads), 0, stream, a, to_args(b),
                        to_args(kv));

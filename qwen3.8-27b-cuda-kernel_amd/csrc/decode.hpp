@@ -47,8 +47,11 @@ struct DecodeArgs {
   const uint16_t* gate;  // bf16, row stride ld_gate
   int ld_gate;
   uint16_t* out;         // [M][nq * 256] bf16
+  // Dynamic block claims (decode_items): balances the decode items against whatever else runs on
+  // the CUs (the ragged launch's prefill units), at the price of run-to-run bit reproducibility:
+  // which wave sums which block changes the fp32 summation order. Off: a fixed schedule.
+  bool dynamic_claims;
 };
-
 
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -513,7 +516,7 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
       BlockSource src;
       const int team = split / kTeam, member = split % kTeam;
       const int slot = item - member;  // the team's first item
-      if (slot < kClaimSlots) {
+      if (a.dynamic_claims && slot < kClaimSlots) {
         const int members = min(kTeam, nsplit - team * kTeam);
         src.tb = team * kTeam * span;
         src.te = min(L, src.tb + members * span);

@@ -193,7 +193,7 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   const int pblocks = int(s.units_bound);
   RaggedArgs r{pblocks, header, pre};
   DecodeArgs d{p.q, p.num_q_heads, p.num_kv_heads, G, p.attn_layer, dec, p.max_splits, target, p.gate, p.ld_gate,
-               p.out};
+               p.out, true};
   PrefillArgs pa{p.q, p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, p.attn_layer};
   const dim3 grid(unsigned(pblocks + dgrid));
   if (kv.dtype == Q38A_KV_INT8)
