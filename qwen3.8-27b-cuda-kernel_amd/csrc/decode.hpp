@@ -608,6 +608,51 @@ __device__ inline void merge_row(const float* src, int splits, size_t stride, co
   *reinterpret_cast<uint2*>(out_row + d) = uint2{uint32_t(o[0]) | (uint32_t(o[1]) << 16), uint32_t(o[2]) | (uint32_t(o[3]) << 16)};
 }
 
+// merge_row for prefill partial rows (kPartialRowFloats: O / l in fp16, then m, l): split s weighs
+// 2^(m_s - M) l_s. One wave; lane l owns dims 4l + [0, 4).
+__device__ inline void merge_row_h16(const float* src, int splits, size_t stride, const uint16_t* gate_row,
+                                     uint16_t* out_row) {
+  const int d = 4 * (threadIdx.x & 63);
+  float M = -INFINITY, wsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
+    uint2 v[kMergeBatch];
+    float2 ml[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const int s = min(s0 + u, splits - 1);
+      const float* p = src + s * stride;
+      v[u] = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + d);
+      ml[u] = *reinterpret_cast<const float2*>(p + kHeadDim / 2);
+      if (s0 + u >= splits) ml[u] = float2{-INFINITY, 0.f};
+    }
+    float bm = M;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) bm = fmaxf(bm, ml[u].x);
+    if (bm == -INFINITY) continue;  // uniform
+    const float c = __builtin_amdgcn_exp2f(M - bm);
+    M = bm;
+    wsum *= c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= c;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const float w = __builtin_amdgcn_exp2f(ml[u].x - M) * ml[u].y;  // empty split: 0
+      const half2_t a = __builtin_bit_cast(half2_t, v[u].x), b = __builtin_bit_cast(half2_t, v[u].y);
+      wsum += w;
+      acc[0] += w * float(a[0]);
+      acc[1] += w * float(a[1]);
+      acc[2] += w * float(b[0]);
+      acc[3] += w * float(b[1]);
+    }
+  }
+  const uint2 g = *reinterpret_cast<const uint2*>(gate_row + d);
+  const uint16_t gv[4] = {uint16_t(g.x), uint16_t(g.x >> 16), uint16_t(g.y), uint16_t(g.y >> 16)};
+  uint16_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = bf16_bits((wsum > 0.f ? acc[i] / wsum : 0.f) * sigmoid_gate(gv[i]));
+  *reinterpret_cast<uint2*>(out_row + d) = uint2{uint32_t(o[0]) | (uint32_t(o[1]) << 16), uint32_t(o[2]) | (uint32_t(o[3]) << 16)};
+}
+
 struct alignas(16) MergeShared {
   float m[kMergeWaves], l[kMergeWaves];
   float acc[kMergeWaves][kHeadDim];

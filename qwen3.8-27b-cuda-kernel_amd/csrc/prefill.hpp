@@ -192,10 +192,15 @@ __device__ inline half4_t v_keys4(const KvTile& T, int key0, int dim0, int j) {
   return __builtin_bit_cast(half4_t, r);
 }
 
+// A split tile's partial row: the normalised output O / l as fp16 (a convex combination of V rows,
+// so within V's range; relative error 2^-11, a twentieth of the output tolerance), then the row's
+// running max m and sum l in fp32, padded to 528 bytes. Half the bytes of an fp32 accumulator row.
+constexpr int kPartialRowFloats = kHeadDim / 2 + 4;
+
 // Row tile `tile` of sequence b and kv head kvh, key blocks [part * kt / parts, (part + 1) * kt / parts)
 // of the tile's kt = ceil(kend / 32) blocks. With parts == 1 the result is final (normalised, gated,
-// bf16 into a.out); otherwise the tile's unnormalised partial goes to `partial`: [128 rows][256 + 2]
-// floats (acc[256], m, l per row in the exp2 domain, m = -inf and l = 0 for a row without keys).
+// bf16 into a.out); otherwise the tile's partial goes to `partial`: [128 rows][kPartialRowFloats]
+// (O / l in fp16, then m, l per row in the exp2 domain; m = -inf and l = 0 for a row without keys).
 template <int DT>
 __device__ __attribute__((always_inline)) inline void prefill_unit(const PrefillArgs& a, const BatchArgs& batch,
                                                                    const KvArgs& kv, KvTile (&tiles)[2], int b,
@@ -337,17 +342,20 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 
   const float lt = l_run + __shfl_xor(l_run, 32, 64);
   if (!row_ok) return;
-  if (parts > 1) {  // partial: row-major [row][256 + 2]; a lane stores its 4-dim runs
-    float* dst = partial + size_t(my_row - r0) * (kHeadDim + 2);
+  if (parts > 1) {  // partial row (kPartialRowFloats): O / l as fp16 [256], then m, l (fp32)
+    float* row = partial + size_t(my_row - r0) * kPartialRowFloats;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(row);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
         const int d = 32 * dt + 8 * blk + 4 * kg;
-        *reinterpret_cast<float2*>(dst + d) = float2{O[dt][4 * blk], O[dt][4 * blk + 1]};
-        *reinterpret_cast<float2*>(dst + d + 2) = float2{O[dt][4 * blk + 2], O[dt][4 * blk + 3]};
+        const half2_t a = {_Float16(O[dt][4 * blk] * inv), _Float16(O[dt][4 * blk + 1] * inv)};
+        const half2_t c = {_Float16(O[dt][4 * blk + 2] * inv), _Float16(O[dt][4 * blk + 3] * inv)};
+        *reinterpret_cast<u32x2*>(dst + d) = u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, c)};
       }
-    if (kg == 0) *reinterpret_cast<float2*>(dst + kHeadDim) = float2{m_run, lt};
+    if (kg == 0) *reinterpret_cast<float2*>(row + kHeadDim / 2) = float2{m_run, lt};
     return;
   }
   // final: O / l * sigmoid(gate) -> bf16

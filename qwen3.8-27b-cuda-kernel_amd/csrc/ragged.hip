@@ -20,7 +20,7 @@
 // workgroup of each kind records what the merge needs in the scratch header.
 //
 // Scratch (floats, q38a_ragged_scratch_floats): header (kHeaderInts ints) | decode partials
-// [B][nq][max_splits][258] | prefill partials [units][128 rows][258].
+// [B][nq][max_splits][258] | prefill partials [units][128 rows][kPartialRowFloats].
 #include "decode.hpp"
 #include "prefill.hpp"
 
@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(kThreads, 2)
       const int tile_r = local / (pa.nkv * parts), rem = local % (pa.nkv * parts);
       const int tile = prefill_tiles(n, pa.group) - 1 - tile_r;
       prefill_unit<DT>(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts, parts,
-                   r.prefill_partials + size_t(u) * kPrefillRows * (kHeadDim + 2));
+                   r.prefill_partials + size_t(u) * kPrefillRows * kPartialRowFloats);
     }
   } else {
     const DecodePlan pl = wave_decode_plan(batch, d.nkv, d.max_splits, d.target_items);
@@ -143,11 +143,11 @@ __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(Ragged
   const int row = kPrefillRows * (prefill_tiles(n, G) - 1 - tile_r) + rt;
   if (row >= n * G) return;
   const size_t unit = size_t(a.header[kUnitPrefix + b]) + size_t(tile_r * a.nkv + kvh) * parts;
-  const size_t unit_floats = size_t(kPrefillRows) * (kHeadDim + 2);
+  const size_t unit_floats = size_t(kPrefillRows) * kPartialRowFloats;
   const int tok = row / G, hq = kvh * G + row % G;
   const size_t m = size_t(batch.seq_start[b] + tok);
-  merge_row(a.prefill_partials + unit * unit_floats + size_t(rt) * (kHeadDim + 2), parts, unit_floats,
-            a.gate + m * a.ld_gate + hq * kHeadDim, a.out + (m * a.nq + hq) * kHeadDim);
+  merge_row_h16(a.prefill_partials + unit * unit_floats + size_t(rt) * kPartialRowFloats, parts, unit_floats,
+                a.gate + m * a.ld_gate + hq * kHeadDim, a.out + (m * a.nq + hq) * kHeadDim);
 }
 
 struct RaggedShape {
@@ -173,7 +173,7 @@ int decode_grid(int* grid, int* target_items);
 
 size_t ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits) {
   const RaggedShape s = ragged_shape(num_seqs, num_tokens, max_tokens_per_seq, nq, nkv, max_splits);
-  return size_t(kHeaderInts) + s.decode_floats + s.units_bound * kPrefillRows * (kHeadDim + 2);
+  return size_t(kHeaderInts) + s.decode_floats + s.units_bound * kPrefillRows * kPartialRowFloats;
 }
 
 int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
