@@ -12,7 +12,7 @@ __global__ void __launch_bounds__(kPThreads, 2) attn_prefill_kernel(PrefillArgs 
   __shared__ KvTile tiles[2];
   const int tiles_x = int(gridDim.x) / a.nkv;
   const int tile = tiles_x - 1 - int(blockIdx.x) / a.nkv, kvh = int(blockIdx.x) % a.nkv;
-  prefill_unit<DT>(a, batch, kv, tiles, blockIdx.y, kvh, tile, 0, 1, nullptr);
+  prefill_unit<DT, DT == Q38A_KV_INT8>(a, batch, kv, tiles, blockIdx.y, kvh, tile, 0, 1, nullptr);
 }
 
 }  // namespace

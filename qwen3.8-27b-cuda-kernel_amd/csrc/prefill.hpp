@@ -201,7 +201,7 @@ constexpr int kPartialRowFloats = kHeadDim / 2 + 4;
 // of the tile's kt = ceil(kend / 32) blocks. With parts == 1 the result is final (normalised, gated,
 // bf16 into a.out); otherwise the tile's partial goes to `partial`: [128 rows][kPartialRowFloats]
 // (O / l in fp16, then m, l per row in the exp2 domain; m = -inf and l = 0 for a row without keys).
-template <int DT>
+template <int DT, bool kLookahead = false>
 __device__ __attribute__((always_inline)) inline void prefill_unit(const PrefillArgs& a, const BatchArgs& batch,
                                                                    const KvArgs& kv, KvTile (&tiles)[2], int b,
                                                                    int kvh, int tile, int part, int parts,
@@ -266,12 +266,33 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 
     // S^T = K . Q^T: element 4 blk + r is key key0 + 8 blk + 4 kg + r of this lane's row
     float16_t S = {};
+    if constexpr (kLookahead) {
+      // Operand reads run kKDepth steps ahead of their MFMA, so an MFMA does not wait for the full
+      // LDS latency of its own operand. The scheduling groups pin that order (they match by
+      // instruction type only: the prologue's reads, then MFMA s and the read for s + kKDepth);
+      // left to itself the compiler reads every operand into one register quad right before use.
+      constexpr int kKDepth = 2;
+      half8_t kb[kKDepth];
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      const half8_t kf = *reinterpret_cast<const half8_t*>(&T.k[col][16 * s + 8 * kg]);
-      S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], S, 0, 0, 0);
-      // bound how far the scheduler hoists operand reads (keeps the live register set small)
-      if ((s & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      for (int s = 0; s < kKDepth; ++s) kb[s] = *reinterpret_cast<const half8_t*>(&T.k[col][16 * s + 8 * kg]);
+      __builtin_amdgcn_sched_group_barrier(0x100, kKDepth, 0);  // the prologue's reads first
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const half8_t kf = kb[s % kKDepth];
+        if (s + kKDepth < 16)
+          kb[s % kKDepth] = *reinterpret_cast<const half8_t*>(&T.k[col][16 * (s + kKDepth) + 8 * kg]);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], S, 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // then MFMA s, read s + depth, ...
+        if (s + kKDepth < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const half8_t kf = *reinterpret_cast<const half8_t*>(&T.k[col][16 * s + 8 * kg]);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], S, 0, 0, 0);
+        // bound how far the scheduler hoists operand reads (keeps the live register set small)
+        if ((s & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
     }
     const bool need_mask = key0 + kKeyTile - 1 > wave_qpos_min;  // wave-uniform
     if (need_mask) {
@@ -311,20 +332,47 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
     l_run = l_run * corr + psum;
     // O^T += V^T . P^T: MFMA step t covers keys 16 t + {0..3, 8..11} (k-group 0) and
     // 16 t + {4..7, 12..15} (k-group 1), matching where P^T already sits
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const half8_t pb = {P[2 * t][0], P[2 * t][1], P[2 * t][2], P[2 * t][3],
-                          P[2 * t + 1][0], P[2 * t + 1][1], P[2 * t + 1][2], P[2 * t + 1][3]};
-      const int kk = 16 * t + 4 * kg;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        // lane: dim 32 dt + col, keys kk + [0, 4) and kk + 8 + [0, 4)
+    if constexpr (kLookahead) {
+      constexpr int kVDepth = 2;  // as for K: reads two MFMAs ahead (two transposing reads each)
+      auto vread = [&](int i) {  // operand i = 8 t + dt
+        const int t = i >> 3, dt = i & 7;
+        const int kk = 16 * t + 4 * kg;
         const int dim0 = 32 * dt + 16 * ((lane >> 4) & 1);
         const half4_t lo = v_keys4(T, kk, dim0, lane & 15);
         const half4_t hi = v_keys4(T, kk + 8, dim0, lane & 15);
-        const half8_t va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      };
+      half8_t vb[kVDepth];
+#pragma unroll
+      for (int i = 0; i < kVDepth; ++i) vb[i] = vread(i);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kVDepth, 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = i >> 3, dt = i & 7;
+        const half8_t pb = {P[2 * t][0], P[2 * t][1], P[2 * t][2], P[2 * t][3],
+                            P[2 * t + 1][0], P[2 * t + 1][1], P[2 * t + 1][2], P[2 * t + 1][3]};
+        const half8_t va = vb[i % kVDepth];
+        if (i + kVDepth < 16) vb[i % kVDepth] = vread(i + kVDepth);
         O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, O[dt], 0, 0, 0);
-        if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i + kVDepth < 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const half8_t pb = {P[2 * t][0], P[2 * t][1], P[2 * t][2], P[2 * t][3],
+                            P[2 * t + 1][0], P[2 * t + 1][1], P[2 * t + 1][2], P[2 * t + 1][3]};
+        const int kk = 16 * t + 4 * kg;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          // lane: dim 32 dt + col, keys kk + [0, 4) and kk + 8 + [0, 4)
+          const int dim0 = 32 * dt + 16 * ((lane >> 4) & 1);
+          const half4_t lo = v_keys4(T, kk, dim0, lane & 15);
+          const half4_t hi = v_keys4(T, kk + 8, dim0, lane & 15);
+          const half8_t va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, O[dt], 0, 0, 0);
+          if ((dt & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
   };
