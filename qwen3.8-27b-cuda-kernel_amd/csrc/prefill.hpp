@@ -137,6 +137,53 @@ __device__ inline void store_tile(KvTile& T, const RawTile& R, int key0, int lim
   dequant_store32(&T.v[key][d0], R.v, live ? __builtin_bit_cast(_Float16, R.vs) : _Float16(0.0f));
 }
 
+// Eight-wave workgroups (512 threads): a thread's share of a raw int8 tile is half as large, the
+// K and V codes of key t % 32, dims 16 (t / 32) + [0, 16), and the scales of their 64-dim group.
+struct RawTile8 {
+  u32x4 k, v;
+  uint16_t ks, vs;
+};
+
+__device__ inline TileOffsets tile_offsets8(const PageLayout& L, int kvh, int tid) {
+  TileOffsets o;
+  const int key = tid & 31, slice = tid >> 5;
+  o.k = int(L.k_row(kvh, key)) + 16 * slice;
+  o.ks = int(L.k_scales(kvh, key)) + 2 * (slice >> 2);
+  o.v = int(L.v_row(kvh, key)) + 16 * slice;
+  o.vs = int(L.v_scales(kvh, key)) + 2 * (slice >> 2);
+  return o;
+}
+
+__device__ inline void load_raw(RawTile8& R, __amdgpu_buffer_rsrc_t pg, int srow, int ssc, const TileOffsets& o) {
+  R.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.k, srow, 0));
+  R.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.v, srow, 0));
+  R.ks = __builtin_amdgcn_raw_buffer_load_b16(pg, o.ks, ssc, 0);
+  R.vs = __builtin_amdgcn_raw_buffer_load_b16(pg, o.vs, ssc, 0);
+}
+
+// 16 codes times one scale -> 16 fp16 at dst (16-byte aligned), as dequant_store32.
+__device__ inline void dequant_store16(uint16_t* dst, const u32x4& w, _Float16 s) {
+  const half2_t sv = {s, s};
+  uint32_t out[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = w[i] ^ 0x80808080u;
+    out[2 * i] = __builtin_bit_cast(uint32_t, dequant_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), sv));
+    out[2 * i + 1] =
+        __builtin_bit_cast(uint32_t, dequant_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), sv));
+  }
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+  d[0] = u32x4{out[0], out[1], out[2], out[3]};
+  d[1] = u32x4{out[4], out[5], out[6], out[7]};
+}
+
+__device__ inline void store_tile(KvTile& T, const RawTile8& R, int key0, int limit, int tid) {
+  const int key = tid & 31, d0 = 16 * (tid >> 5);
+  const bool live = key0 + key < limit;
+  dequant_store16(&T.k[key][d0], R.k, live ? __builtin_bit_cast(_Float16, R.ks) : _Float16(0.0f));
+  dequant_store16(&T.v[key][d0], R.v, live ? __builtin_bit_cast(_Float16, R.vs) : _Float16(0.0f));
+}
+
 // bf16 pages: one thread's share of a raw tile (K and V of key t % 32, dims 32 (t / 32) + [0, 32)).
 struct RawTileBf16 {
   u32x4 k[4], v[4];
@@ -201,7 +248,7 @@ constexpr int kPartialRowFloats = kHeadDim / 2 + 4;
 // of the tile's kt = ceil(kend / 32) blocks. With parts == 1 the result is final (normalised, gated,
 // bf16 into a.out); otherwise the tile's partial goes to `partial`: [128 rows][kPartialRowFloats]
 // (O / l in fp16, then m, l per row in the exp2 domain; m = -inf and l = 0 for a row without keys).
-template <int DT, bool kLookahead = false>
+template <int DT, bool kLookahead = false, int kWavesWG = kPWaves>
 __device__ __attribute__((always_inline)) inline void prefill_unit(const PrefillArgs& a, const BatchArgs& batch,
                                                                    const KvArgs& kv, KvTile (&tiles)[2], int b,
                                                                    int kvh, int tile, int part, int parts,
@@ -212,12 +259,14 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
   const int s0 = batch.seq_start[b];
   const int n = batch.seq_start[b + 1] - s0;
   const int rows = n * G;
-  const int r0 = tile * kRowsPerTile;
+  static_assert(kWavesWG == kPWaves || (kWavesWG == 8 && DT == Q38A_KV_INT8), "eight-wave tiles: int8 pages");
+  constexpr int kTileRows = kWavesWG * kRowsPerWave;
+  const int r0 = tile * kTileRows;
   if (r0 >= rows) return;
   const int pos0 = batch.seq_pos0[b];
   const int* bt = kv.block_table + size_t(batch.seq_slot[b]) * kv.max_pages_per_seq;
   const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
-  const int last_row = min(rows, r0 + kRowsPerTile) - 1;
+  const int last_row = min(rows, r0 + kTileRows) - 1;
   const int kend = pos0 + last_row / G + 1;  // keys [0, kend) are needed by this workgroup
   const int kt = (kend + kKeyTile - 1) / kKeyTile;
   const int jb = part * kt / parts, je = (part + 1) * kt / parts;  // this unit's key blocks
@@ -249,13 +298,14 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 
   // The next tile's raw bytes are loaded into registers while the current tile is computed from
   // LDS, then dequantised into the other LDS buffer.
-  using Raw = std::conditional_t<DT == Q38A_KV_INT8, RawTile, RawTileBf16>;
+  using Raw = std::conditional_t<DT == Q38A_KV_INT8, std::conditional_t<kWavesWG == 8, RawTile8, RawTile>, RawTileBf16>;
   constexpr int kRowBytes = DT == Q38A_KV_INT8 ? kHeadDim : 2 * kHeadDim;
   Raw R;
   // page ids through the constant address space: scalar loads, so a tile's page is a scalar base
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
   auto page_ptr = [&](int key0) { return layer + size_t(btc[key0 / kPageTokens]) * kv.page_bytes; };
-  const TileOffsets toff = DT == Q38A_KV_INT8 ? tile_offsets(kv.layout, kvh, tid) : tile_offsets_bf16(kv.layout, kvh, tid);
+  const TileOffsets toff = DT == Q38A_KV_INT8 ? (kWavesWG == 8 ? tile_offsets8(kv.layout, kvh, tid) : tile_offsets(kv.layout, kvh, tid))
+                                              : tile_offsets_bf16(kv.layout, kvh, tid);
   auto fetch = [&](Raw& RT, int j) {
     if (j < je) {  // uniform
       const int in_page = (j * kKeyTile) % kPageTokens;

@@ -80,3 +80,13 @@ def test_prefill_config3_shape(orc):
     checks 40 tokens spread over the chunk, first and last included."""
     toks = sorted(set([0, 1, 2, 47, 48, 63, 64, 1000, 2046, 2047] + list(range(5, 2048, 70))))
     prefill_step(orc, [(6000, 2048)], seed=3, check_tokens=[toks])
+
+
+def test_prefill_ragged_batch_256_row_tiles(orc):
+    """Enough rows that the launch takes 256-row workgroups (1,556 tokens x 6 heads x 4 kv heads
+    / 128 > 256 CUs): ragged lengths, a 1-token row and tiles that end mid-sequence; the oracle
+    checks a spread of tokens of every sequence, first and last included."""
+    seqs = [(0, 700), (130, 555), (4000, 300), (64, 1)]
+    checks = [sorted(set([0, 1, 42, 43, 85, 86, 699] + list(range(3, n, 37)))) if n > 1 else [0] for _, n in seqs]
+    checks = [[t for t in c if t < n] for c, (_, n) in zip(checks, seqs)]
+    prefill_step(orc, seqs, seed=77, check_tokens=checks)
