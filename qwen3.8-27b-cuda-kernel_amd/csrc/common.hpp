@@ -92,6 +92,13 @@ __host__ __device__ inline uint16_t bf16_bits(float f) {
 }
 __host__ __device__ inline float bf16_value(uint16_t b) { return as_f32(uint32_t(b) << 16); }
 
+// sigmoid(g) = 1 / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal (each within ~1 ulp):
+// the gated outputs are rounded to bf16 (8 significand bits), so the libm-accurate forms bought
+// nothing and cost ~25 instructions per element in the epilogues. g -> -inf gives 0, +inf gives 1.
+__device__ inline float fast_sigmoid(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504088896341f * g));
+}
+
 // ---- MFMA operand types (gfx950) ----------------------------------------------------------------
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -123,6 +130,7 @@ inline BatchArgs to_args(const q38a_batch_desc& b) {
   return BatchArgs{b.num_seqs, b.num_tokens, b.max_tokens_per_seq, b.seq_start,
                    b.seq_slot, b.seq_pos0,   b.tok_pos,            b.tok_seq};
 }
+
 inline KvArgs to_args(const q38a_kv_cache_desc& k) {
   return KvArgs{k.pool, PageLayout{k.kv_heads, k.dtype}, k.num_pages, k.page_bytes, k.layer_stride,
                 k.block_table, k.max_pages_per_seq};

@@ -555,7 +555,7 @@ __device__ inline float wave_sum(float x) {
   return x;
 }
 
-__device__ inline float sigmoid_gate(uint16_t g) { return 1.0f / (1.0f + expf(-bf16_value(g))); }
+__device__ inline float sigmoid_gate(uint16_t g) { return fast_sigmoid(bf16_value(g)); }
 
 // Folds the splits s = first, first + step, ... (< splits) of one (row, q head) into a running
 // log-sum-exp state (M, lsum, acc[4] of dims d..d+3), kMergeBatch splits in flight per lane.

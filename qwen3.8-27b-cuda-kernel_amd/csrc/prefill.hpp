@@ -32,6 +32,11 @@
 namespace q38a {
 namespace {
 
+// p[i] through the constant address space (read-only launch metadata): a scalar load
+__device__ inline int const_load(const int* p, int i) {
+  return reinterpret_cast<const __attribute__((address_space(4))) int*>(reinterpret_cast<uintptr_t>(p))[i];
+}
+
 constexpr int kPWaves = 4;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kRowsPerWave = 32;
@@ -256,15 +261,17 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.group;
-  const int s0 = batch.seq_start[b];
-  const int n = batch.seq_start[b + 1] - s0;
+  // launch metadata through the constant address space: scalar loads, wave-uniform values (a vector
+  // load after a store in the same launch would make every bound derived from it divergent)
+  const int s0 = const_load(batch.seq_start, b);
+  const int n = const_load(batch.seq_start, b + 1) - s0;
   const int rows = n * G;
   static_assert(kWavesWG == kPWaves || (kWavesWG == 8 && DT == Q38A_KV_INT8), "eight-wave tiles: int8 pages");
   constexpr int kTileRows = kWavesWG * kRowsPerWave;
   const int r0 = tile * kTileRows;
   if (r0 >= rows) return;
-  const int pos0 = batch.seq_pos0[b];
-  const int* bt = kv.block_table + size_t(batch.seq_slot[b]) * kv.max_pages_per_seq;
+  const int pos0 = const_load(batch.seq_pos0, b);
+  const int* bt = kv.block_table + size_t(const_load(batch.seq_slot, b)) * kv.max_pages_per_seq;
   const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
   const int last_row = min(rows, r0 + kTileRows) - 1;
   const int kend = pos0 + last_row / G + 1;  // keys [0, kend) are needed by this workgroup
@@ -472,8 +479,8 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const float g0 = bf16_value(uint16_t(gw[h])), g1 = bf16_value(uint16_t(gw[h] >> 16));
-        const float y0 = O[dt][4 * blk + 2 * h] * inv * (1.0f / (1.0f + expf(-g0)));
-        const float y1 = O[dt][4 * blk + 2 * h + 1] * inv * (1.0f / (1.0f + expf(-g1)));
+        const float y0 = O[dt][4 * blk + 2 * h] * inv * fast_sigmoid(g0);
+        const float y1 = O[dt][4 * blk + 2 * h + 1] * inv * fast_sigmoid(g1);
         o[h] = uint32_t(bf16_bits(y0)) | (uint32_t(bf16_bits(y1)) << 16);
       }
       *reinterpret_cast<u32x2*>(orow + d) = u32x2{o[0], o[1]};
