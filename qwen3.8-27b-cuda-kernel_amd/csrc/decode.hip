@@ -15,7 +15,7 @@ __device__ int g_chunk_pages;
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads, 2) attn_decode_kernel(DecodeArgs a, BatchArgs batch, KvArgs kv) {
-  __shared__ DecodeShared sh;
+  __shared__ DecodeShared<> sh;
   const DecodePlan pl = wave_decode_plan(batch, a.nkv, a.max_splits, a.target_items);
   if (blockIdx.x == 0 && threadIdx.x == 0) g_chunk_pages = pl.cp;
   decode_items<DT>(a, batch, kv, pl, sh, blockIdx.x, gridDim.x);

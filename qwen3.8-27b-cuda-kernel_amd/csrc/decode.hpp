@@ -323,6 +323,7 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
 }
 
 // bf16 pages: keys [t_begin, t_end), each wave takes 16-token blocks in turn from global memory.
+template <int W>
 __device__ void decode_item_bf16(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, int q_row,
                                  int t_begin, int t_end, float& m_run, float& l_run, float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63;
@@ -354,7 +355,7 @@ __device__ void decode_item_bf16(const DecodeArgs& a, const KvArgs& kv, const in
       qb[g][h] = v;
       qb_lo[g][h] = vl;
     }
-  for (int blk = wave; blk < nblk; blk += kWaves) {
+  for (int blk = wave; blk < nblk; blk += W) {
     const int t0 = t_begin + 16 * blk;
     const uint8_t* pg = layer + size_t(bt[t0 / kPageTokens]) * kv.page_bytes;
     const int in0 = t0 % kPageTokens;
@@ -420,19 +421,21 @@ __device__ inline int tile_dim4(int k4, int n) {
   else return 16 * n + 4 * k4;
 }
 
+template <int W>
 struct alignas(16) WaveMerge {
-  float o[kWaves][kMaxGroup][kHeadDim];
-  float m[kWaves][kMaxGroup];
-  float l[kWaves][kMaxGroup];
+  float o[W][kMaxGroup][kHeadDim];
+  float m[W][kMaxGroup];
+  float l[W][kMaxGroup];
 };
 
+template <int W = kWaves>
 struct alignas(16) DecodeShared {
-  WaveMerge merge;  // the 4 waves' state at the end of an item
+  WaveMerge<W> merge;  // the W waves' state at the end of an item
 };
 
-// Merges the 4 waves' (m, l, O) of an item in LDS and writes the item's partial to scratch.
-template <int DT>
-__device__ void finish_item(const DecodeArgs& a, WaveMerge& sm, int b, int kvh, int split, float m_run, float l_run,
+// Merges the W waves' (m, l, O) of an item in LDS and writes the item's partial to scratch.
+template <int DT, int W>
+__device__ void finish_item(const DecodeArgs& a, WaveMerge<W>& sm, int b, int kvh, int split, float m_run, float l_run,
                             const float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = a.group;
@@ -454,14 +457,14 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge& sm, int b, int kvh, 
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += 64 * W) {
     const int g = idx / kHeadDim, d = idx % kHeadDim;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm.m[w][g]);
+    for (int w = 0; w < W; ++w) M = fmaxf(M, sm.m[w][g]);
     float acc = 0.f, lsum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float f = sm.m[w][g] == -INFINITY ? 0.f : exp2f(sm.m[w][g] - M);
       acc += f * sm.o[w][g][d];
       lsum += f * sm.l[w][g];
@@ -492,10 +495,10 @@ __device__ int g_claims[kClaimSlots * kClaimStride];
 // over the XCDs; teams of kTeam of them share a claim counter over their pages (int8 pages; the
 // items of one row are consecutive, so a team's items are items slot .. slot + members - 1).
 // Partials go to a.scratch.
-template <int DT>
+template <int DT, int W = kWaves>
 __device__ __attribute__((always_inline)) inline void decode_items(const DecodeArgs& a, const BatchArgs& batch,
                                                                    const KvArgs& kv, const DecodePlan& pl,
-                                                                   DecodeShared& sh, int wg, int nwg) {
+                                                                   DecodeShared<W>& sh, int wg, int nwg) {
   const int cp = pl.cp;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   for (int item = wg;; item += nwg) {
@@ -520,8 +523,8 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
         const int members = min(kTeam, nsplit - team * kTeam);
         src.tb = team * kTeam * span;
         src.te = min(L, src.tb + members * span);
-        src.first = member * kWaves + wave;
-        src.base = members * kWaves;
+        src.first = member * W + wave;
+        src.base = members * W;
         src.ctr = &g_claims[slot * kClaimStride];
       } else {
         src.tb = split * span;
@@ -530,13 +533,13 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
         src.ctr = nullptr;
       }
       src.nblk = ceil_div_i(src.te - src.tb, 16);
-      src.stride = kWaves;
+      src.stride = W;
       decode_item_int8(a, kv, bt, kvh, q_row, src, m_run, l_run, O);
     } else {
       const int t_begin = split * span;
-      decode_item_bf16(a, kv, bt, kvh, q_row, t_begin, min(L, t_begin + span), m_run, l_run, O);
+      decode_item_bf16<W>(a, kv, bt, kvh, q_row, t_begin, min(L, t_begin + span), m_run, l_run, O);
     }
-    finish_item<DT>(a, sh.merge, b, kvh, split, m_run, l_run, O);
+    finish_item<DT, W>(a, sh.merge, b, kvh, split, m_run, l_run, O);
   }
 }
 

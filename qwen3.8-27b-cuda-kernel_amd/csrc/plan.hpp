@@ -15,7 +15,7 @@
 
 namespace q38a {
 
-constexpr int kPlanThreads = 256;
+constexpr int kPlanThreads = 512;  // the ragged launch's workgroup (eight waves)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kScoreScale = kLog2e / 16.0f;  // 1/sqrt(256) folded into the exp2 domain
 constexpr int kMaxSeqs = 1024;  // sequences per step accepted by the attention launchers
@@ -176,7 +176,7 @@ __device__ inline ItemSpot wave_locate(const BatchArgs& batch, int nkv, const De
 // within `target` (one wave of resident workgroups) instead of spilling a short second wave.
 // Unit order: sequences in batch order; inside a sequence (tile from last to first, kv head, part),
 // so the longest rows start first.
-constexpr int kPrefillRows = 128;
+constexpr int kPrefillRows = 256;  // rows of a ragged-launch prefill unit (eight waves of 32)
 constexpr int kKeyTile = 32;
 
 __device__ inline int prefill_len(const BatchArgs& b, int s) {

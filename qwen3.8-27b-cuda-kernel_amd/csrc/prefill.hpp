@@ -41,7 +41,7 @@ constexpr int kPWaves = 4;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kRowsPerWave = 32;
 constexpr int kRowsPerTile = kPWaves * kRowsPerWave;  // 128 (token, head) rows per workgroup
-static_assert(kRowsPerTile == kPrefillRows, "prefill row tile");
+static_assert(2 * kRowsPerTile == kPrefillRows, "ragged prefill units are eight-wave tiles");
 // LDS row strides (halves). K rows are read 16 B per lane by 32 different keys (528 B apart: 16
 // consecutive keys cover all banks once). V rows are read by ds_read_b64_tr_b16, four rows of 32 B
 // per 16 lanes. Both are written 16 B per lane by 32 consecutive keys; for the V rows the stride
@@ -227,6 +227,51 @@ __device__ inline void bf16_store32(uint16_t* dst, const u32x4 (&w)[4], bool liv
   }
 }
 
+// Eight-wave workgroups, bf16 pages: key t % 32, dims 16 (t / 32) + [0, 16) of K and V.
+struct RawTileBf16x8 {
+  u32x4 k[2], v[2];
+};
+
+__device__ inline TileOffsets tile_offsets_bf16x8(const PageLayout& L, int kvh, int tid) {
+  TileOffsets o;
+  const int key = tid & 31, slice = tid >> 5;
+  o.k = int(L.k_row(kvh, key)) + 32 * slice;
+  o.v = int(L.v_row(kvh, key)) + 32 * slice;
+  o.ks = o.vs = 0;
+  return o;
+}
+
+__device__ inline void load_raw(RawTileBf16x8& R, __amdgpu_buffer_rsrc_t pg, int srow, int, const TileOffsets& o) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    R.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.k, srow + 16 * i, 0));
+    R.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.v, srow + 16 * i, 0));
+  }
+}
+
+// 16 bf16 values -> fp16 at dst, as bf16_store32.
+__device__ inline void bf16_store16(uint16_t* dst, const u32x4 (&w)[2], bool live) {
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = w[c][i];
+      const half2_t h = {_Float16(__uint_as_float(x << 16)), _Float16(__uint_as_float(x & 0xffff0000u))};
+      o[i] = live ? __builtin_bit_cast(uint32_t, h) : 0u;
+    }
+    d[c] = o;
+  }
+}
+
+__device__ inline void store_tile(KvTile& T, const RawTileBf16x8& R, int key0, int limit, int tid) {
+  const int key = tid & 31, d0 = 16 * (tid >> 5);
+  const bool live = key0 + key < limit;
+  bf16_store16(&T.k[key][d0], R.k, live);
+  bf16_store16(&T.v[key][d0], R.v, live);
+}
+
 __device__ inline void store_tile(KvTile& T, const RawTileBf16& R, int key0, int limit, int tid) {
   const int key = tid & 31, d0 = 32 * (tid >> 5);
   const bool live = key0 + key < limit;
@@ -266,7 +311,7 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
   const int s0 = const_load(batch.seq_start, b);
   const int n = const_load(batch.seq_start, b + 1) - s0;
   const int rows = n * G;
-  static_assert(kWavesWG == kPWaves || (kWavesWG == 8 && DT == Q38A_KV_INT8), "eight-wave tiles: int8 pages");
+  static_assert(kWavesWG == kPWaves || kWavesWG == 8, "four- or eight-wave workgroups");
   constexpr int kTileRows = kWavesWG * kRowsPerWave;
   const int r0 = tile * kTileRows;
   if (r0 >= rows) return;
@@ -305,14 +350,16 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 
   // The next tile's raw bytes are loaded into registers while the current tile is computed from
   // LDS, then dequantised into the other LDS buffer.
-  using Raw = std::conditional_t<DT == Q38A_KV_INT8, std::conditional_t<kWavesWG == 8, RawTile8, RawTile>, RawTileBf16>;
+  using Raw = std::conditional_t<DT == Q38A_KV_INT8, std::conditional_t<kWavesWG == 8, RawTile8, RawTile>,
+                                 std::conditional_t<kWavesWG == 8, RawTileBf16x8, RawTileBf16>>;
   constexpr int kRowBytes = DT == Q38A_KV_INT8 ? kHeadDim : 2 * kHeadDim;
   Raw R;
   // page ids through the constant address space: scalar loads, so a tile's page is a scalar base
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
   auto page_ptr = [&](int key0) { return layer + size_t(btc[key0 / kPageTokens]) * kv.page_bytes; };
-  const TileOffsets toff = DT == Q38A_KV_INT8 ? (kWavesWG == 8 ? tile_offsets8(kv.layout, kvh, tid) : tile_offsets(kv.layout, kvh, tid))
-                                              : tile_offsets_bf16(kv.layout, kvh, tid);
+  const TileOffsets toff =
+      DT == Q38A_KV_INT8 ? (kWavesWG == 8 ? tile_offsets8(kv.layout, kvh, tid) : tile_offsets(kv.layout, kvh, tid))
+                         : (kWavesWG == 8 ? tile_offsets_bf16x8(kv.layout, kvh, tid) : tile_offsets_bf16(kv.layout, kvh, tid));
   auto fetch = [&](Raw& RT, int j) {
     if (j < je) {  // uniform
       const int in_page = (j * kKeyTile) % kPageTokens;

@@ -6,8 +6,11 @@
 // decode rows and attention_prefill (src/kernels/attention_prefill.cu:154-313) for the chunks; the
 // reference runs them as separate launches (src/engine.cpp:133-182).
 //
-// Launch layout: grid = P prefill workgroups followed by D = 2 x CUs decode workgroups, all 256
-// threads with the same register and LDS budget, so both kinds share the CUs. Workgroups are
+// Launch layout: grid = P prefill workgroups followed by D = CUs decode workgroups, all eight waves
+// (512 threads) with the same register and LDS budget (one workgroup per CU), so both kinds share
+// the CUs. Eight waves let a prefill unit stage each key tile once for 256 rows (half the staging
+// per thread of four-wave units, the registers for the operand lookahead) and a decode item spread
+// over eight waves. Workgroups are
 // dispatched in index order, so the long prefill units start first and the short, HBM-bound decode
 // items fill in behind them.
 //   * prefill: every (row tile, kv head) of a chunk is cut into parts of about the same number of key
@@ -20,14 +23,16 @@
 // workgroup of each kind records what the merge needs in the scratch header.
 //
 // Scratch (floats, q38a_ragged_scratch_floats): header (kHeaderInts ints) | decode partials
-// [B][nq][max_splits][258] | prefill partials [units][128 rows][kPartialRowFloats].
+// [B][nq][max_splits][258] | prefill partials [units][256 rows][kPartialRowFloats].
 #include "decode.hpp"
 #include "prefill.hpp"
 
 namespace q38a {
 namespace {
 
-constexpr int kPrefillTarget = 512;  // prefill units aimed for per launch (2 per CU on MI355X)
+constexpr int kPrefillTarget = 256;  // prefill units aimed for per launch (one per CU on MI355X)
+constexpr int kRaggedWaves = 8;
+constexpr int kRaggedThreads = 64 * kRaggedWaves;
 constexpr int kMinChunk = 16;        // key blocks per part at least (512 keys)
 constexpr int kHeaderInts = 4096;
 // header: [0] decode pages per item, [1] prefill key blocks per part,
@@ -50,13 +55,13 @@ __device__ inline int parts_of(const BatchArgs& batch, int s, int chunk) {
 }
 
 template <int DT>
-__global__ void __launch_bounds__(kThreads, 2)
+__global__ void __launch_bounds__(kRaggedThreads, 1)
     attn_ragged_kernel(RaggedArgs r, DecodeArgs d, PrefillArgs pa, BatchArgs batch, KvArgs kv) {
-  static_assert(kThreads == kPThreads && kThreads == kPlanThreads, "one block shape for both kinds");
+  static_assert(kRaggedThreads == 2 * kPThreads && kRaggedThreads == kPlanThreads, "one block shape for both kinds");
   __shared__ PlanShared plan;
   __shared__ union alignas(16) Work {
     KvTile tiles[2];
-    DecodeShared dec;
+    DecodeShared<kRaggedWaves> dec;
   } sh;
   const int B = batch.num_seqs;
   if (int(blockIdx.x) < r.prefill_blocks) {
@@ -84,14 +89,15 @@ __global__ void __launch_bounds__(kThreads, 2)
       const int parts = parts_of(batch, b, chunk);
       const int tile_r = local / (pa.nkv * parts), rem = local % (pa.nkv * parts);
       const int tile = prefill_tiles(n, pa.group) - 1 - tile_r;
-      prefill_unit<DT>(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts, parts,
-                   r.prefill_partials + size_t(u) * kPrefillRows * kPartialRowFloats);
+      prefill_unit<DT, DT == Q38A_KV_INT8, kRaggedWaves>(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts,
+                                                         parts,
+                                                         r.prefill_partials + size_t(u) * kPrefillRows * kPartialRowFloats);
     }
   } else {
     const DecodePlan pl = wave_decode_plan(batch, d.nkv, d.max_splits, d.target_items);
     const int wg = int(blockIdx.x) - r.prefill_blocks;
     if (wg == 0 && threadIdx.x == 0) r.header[0] = pl.cp;
-    decode_items<DT>(d, batch, kv, pl, sh.dec, wg, int(gridDim.x) - r.prefill_blocks);
+    decode_items<DT, kRaggedWaves>(d, batch, kv, pl, sh.dec, wg, int(gridDim.x) - r.prefill_blocks);
   }
 }
 
@@ -159,7 +165,7 @@ RaggedShape ragged_shape(int num_seqs, int num_tokens, int max_tokens_per_seq, i
   s.decode_floats = size_t(num_seqs) * nq * max_splits * (kHeadDim + 2);
   if (max_tokens_per_seq > 1) {
     const size_t G = size_t(nq / nkv);
-    // sum_b ceil(n_b G / 128) <= M G / 128 + B tiles per kv head; max(1, floor(kt / chunk)) parts per
+    // sum_b ceil(n_b G / 256) <= M G / 256 + B tiles per kv head; max(1, floor(kt / chunk)) parts per
     // tile add at most kPrefillTarget units
     s.tasks_bound = size_t(nkv) * ((size_t(num_tokens) * G) / kPrefillRows + size_t(num_seqs));
     s.units_bound = s.tasks_bound + kPrefillTarget;
@@ -168,8 +174,6 @@ RaggedShape ragged_shape(int num_seqs, int num_tokens, int max_tokens_per_seq, i
 }
 
 }  // namespace
-
-int decode_grid(int* grid, int* target_items);
 
 size_t ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits) {
   const RaggedShape s = ragged_shape(num_seqs, num_tokens, max_tokens_per_seq, nq, nkv, max_splits);
@@ -185,8 +189,11 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   const int G = p.num_q_heads / p.num_kv_heads;
   const RaggedShape s = ragged_shape(b.num_seqs, b.num_tokens, b.max_tokens_per_seq, p.num_q_heads, p.num_kv_heads,
                                      p.max_splits);
-  int dgrid = 0, target = 0;
-  if (int rc = decode_grid(&dgrid, &target)) return rc;
+  int cus = 0;
+  if (int rc = device_cu_count(&cus)) return rc;
+  // one eight-wave decode workgroup per CU, two items each (one item per workgroup: 54 vs 49 us for
+  // config 4's decode rows alone; three: 55)
+  const int dgrid = cus, target = 2 * cus;
   int* header = reinterpret_cast<int*>(p.split_scratch);
   float* dec = p.split_scratch + kHeaderInts;
   float* pre = dec + s.decode_floats;
@@ -197,10 +204,10 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   PrefillArgs pa{p.q, p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, p.attn_layer};
   const dim3 grid(unsigned(pblocks + dgrid));
   if (kv.dtype == Q38A_KV_INT8)
-    hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_INT8>, grid, dim3(kThreads), 0, stream, r, d, pa, to_args(b),
+    hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_INT8>, grid, dim3(kRaggedThreads), 0, stream, r, d, pa, to_args(b),
                        to_args(kv));
   else
-    hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_BF16>, grid, dim3(kThreads), 0, stream, r, d, pa, to_args(b),
+    hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_BF16>, grid, dim3(kRaggedThreads), 0, stream, r, d, pa, to_args(b),
                        to_args(kv));
   if (int rc = check_hip(hipGetLastError(), "attention_ragged launch")) return rc;
   RaggedMergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, header, dec, pre, p.max_splits};

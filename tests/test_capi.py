@@ -82,11 +82,11 @@ def test_rope_table_rejects_other_rotary_dims():
 
 
 def test_ragged_scratch_size_and_refusals():
-    # header (4096 ints) + decode partials [B][nq][splits][258] fp32 + prefill units (tiles bound + 512)
-    # x 128 rows x 132 floats (fp16 O / l [256], m, l, pad)
+    # header (4096 ints) + decode partials [B][nq][splits][258] fp32 + prefill units (tiles bound + 256)
+    # x 256 rows x 132 floats (fp16 O / l [256], m, l, pad)
     B, M, nq, nkv, splits = 8, 519, 24, 4, 64
-    tiles = nkv * (M * (nq // nkv) // 128 + B)
-    want = 4096 + B * nq * splits * 258 + (tiles + 512) * 128 * 132
+    tiles = nkv * (M * (nq // nkv) // 256 + B)
+    want = 4096 + B * nq * splits * 258 + (tiles + 256) * 256 * 132
     assert q38a.ragged_scratch_floats(B, M, 512, nq, nkv, splits) == want
     # all-decode batches need no prefill partials
     assert q38a.ragged_scratch_floats(B, B, 1, nq, nkv, splits) == 4096 + B * nq * splits * 258
