@@ -79,7 +79,9 @@ int q38a_runner_bucket_for(int n, int max_batch);
  * (reference ModelRunner::decode, src/model_runner.cpp:488-532). */
 int q38a_runner_decode(q38a_runner* r, const q38a_step_seq* rows, int n, void* stream);
 
-/* One prefill chunk of every attention layer (reference ModelRunner::prefill, eager). */
+/* One prefill chunk of every attention layer (reference ModelRunner::prefill, eager). Chunks of two
+ * or more tokens use the ragged attention launch (it splits long key ranges over workgroups), a
+ * one-token chunk the prefill launch. */
 int q38a_runner_prefill(q38a_runner* r, int slot, int pos0, int n, void* stream);
 
 /* One mixed step: any sequences (n == 1 decode rows, n > 1 chunks), one ragged attention launch

@@ -3,8 +3,8 @@
 Runner (reference src/model_runner.cpp:488-560): a decode step replayed from its bucket's hipGraph
 gives the same bytes as the eager launches, on every replay, with other eager steps (and other
 buckets) in between; the output of the last layer matches the oracle's exact attention over the
-pages the runner wrote. A mixed ragged step gives the same appended K/V bytes as a prefill launch
-plus a decode launch and outputs within the north star's tolerance.
+pages the runner wrote. A mixed ragged step gives the same appended K/V bytes as a prefill step
+plus a decode step and outputs within the north star's tolerance.
 
 Engine (reference src/engine.cpp:62-184): requests run to completion under both policies with the
 reference's accounting (every prompt token prefilled once, max_new - 1 decode rows per request,
@@ -125,7 +125,7 @@ def test_runner_mixed_step_matches_separate_launches(orc):
     chunk = (3, ctxs[3], 200)
     ddata = randn_bf16(rig.rng, (2, 3, LD))
     cdata = randn_bf16(rig.rng, (2, 200, LD))
-    # reference policy: prefill launch, then the decode launch
+    # reference policy: a prefill step, then a decode step
     rig.fill(rig.b.prefill_row, 200, cdata)
     rig.fill(0, 3, ddata)
     rig.r.prefill(*chunk, rig.s)
