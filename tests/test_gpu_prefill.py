@@ -82,11 +82,12 @@ def test_prefill_config3_shape(orc):
     prefill_step(orc, [(6000, 2048)], seed=3, check_tokens=[toks])
 
 
-def test_prefill_ragged_batch_256_row_tiles(orc):
+@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16])
+def test_prefill_ragged_batch_256_row_tiles(orc, kv_dtype):
     """Enough rows that the launch takes 256-row workgroups (1,556 tokens x 6 heads x 4 kv heads
     / 128 > 256 CUs): ragged lengths, a 1-token row and tiles that end mid-sequence; the oracle
     checks a spread of tokens of every sequence, first and last included."""
     seqs = [(0, 700), (130, 555), (4000, 300), (64, 1)]
     checks = [sorted(set([0, 1, 42, 43, 85, 86, 699] + list(range(3, n, 37)))) if n > 1 else [0] for _, n in seqs]
     checks = [[t for t in c if t < n] for c, (_, n) in zip(checks, seqs)]
-    prefill_step(orc, seqs, seed=77, check_tokens=checks)
+    prefill_step(orc, seqs, seed=77, kv_dtype=kv_dtype, check_tokens=checks)
