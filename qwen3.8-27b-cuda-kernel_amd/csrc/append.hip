@@ -10,7 +10,7 @@
 // Work mapping (MI355X-first): one wave64 per (token, head row); rows are the nq q heads, then the
 // nkv k heads, then the nkv v heads of a token. Lane l owns dims [4l, 4l + 4), so a 64-dim
 // quantisation group is exactly 16 lanes (one DPP row) and RoPE partners (i, i + 32) sit 8 lanes
-// apart. Contraction is off for the whole file and division / square root go through binary64, so
+// apart. Contraction is off for the whole file and division / square root are correctly rounded, so
 // every operation rounds exactly as the reference's IEEE single-precision code does. cos/sin come
 // from a host-built table (same libm calls as the CPU reference), read per position.
 //
@@ -27,12 +27,15 @@
 namespace q38a {
 namespace {
 
-// Correctly rounded binary32 division and square root, computed in binary64 and rounded once:
-// for these operations a 53-bit intermediate (>= 2 * 24 + 2 bits) makes the double rounding
-// innocuous, so the result equals the IEEE single-precision operation whatever fast-math
-// defaults the device library applies to float sqrt/div.
-__device__ inline float div_rn(float a, float b) { return float(double(a) / double(b)); }
-__device__ inline float sqrt_rn(float a) { return float(__builtin_sqrt(double(a))); }
+// Correctly rounded binary32 division and square root, as the reference's IEEE single-precision
+// code computes them: HIP compiles fp32 division and sqrtf to correctly rounded sequences
+// (-fhip-fp32-correctly-rounded-divide-sqrt, clang's default, which the build keeps), at a
+// fraction of the cost of the binary64 operations (the quantiser divides every element).
+#ifdef __FAST_MATH__
+#error "the append must round division and square root correctly: build without fast-math"
+#endif
+__device__ inline float div_rn(float a, float b) { return a / b; }
+__device__ inline float sqrt_rn(float a) { return __builtin_sqrtf(a); }
 
 constexpr int kWavesPerBlock = 4;
 
@@ -60,23 +63,26 @@ struct AppendArgs {
   int rope_rows;
 };
 
-__global__ void __launch_bounds__(kWavesPerBlock * 64)
-qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
-  __shared__ float stage[kWavesPerBlock][kHeadDim];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int job = blockIdx.x * kWavesPerBlock + wave;
-  if (job >= jobs) return;
-  const int rows = p.nq + 2 * p.nkv;
-  const int m = job / rows, r = job % rows;
-  const bool is_q = r < p.nq, is_k = !is_q && r < p.nq + p.nkv;
-  // q head r at column r*256; k head h at (2nq + h)*256; v head h at (2nq + nkv + h)*256
-  const int col = (is_q ? r : p.nq + r) * kHeadDim;
-  const int pos = batch.tok_pos[m];
+// Per-row loads, issued for all of a wave's rows before any row is computed (each row's chain is
+// proj + position, then the RoPE row, then tok_seq -> seq_slot -> block_table for a k or v row).
+struct RowLoads {
+  int m, r, pos;
+  uint2 raw;
+  float4 c4, s4;
+  int page;
+  bool store_ok;
+};
 
-  const uint2 raw = *reinterpret_cast<const uint2*>(p.proj + size_t(m) * p.ld_proj + col + 4 * lane);
+// One (token, head row): norm, RoPE, then the q store or the page-row store, from its loads.
+__device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, float* stage, int lane, const RowLoads& L) {
+  const int m = L.m, r = L.r, pos = L.pos, page = L.page;
+  const bool store_ok = L.store_ok;
+  const uint2 raw = L.raw;
+  const float4 c4 = L.c4, s4 = L.s4;
+  const bool is_q = r < p.nq, is_k = !is_q && r < p.nq + p.nkv;
+  const bool pos_ok = pos >= 0 && pos < p.rope_rows;
   float x[4] = {bf16_value(uint16_t(raw.x)), bf16_value(uint16_t(raw.x >> 16)), bf16_value(uint16_t(raw.y)),
                 bf16_value(uint16_t(raw.y >> 16))};
-  const bool pos_ok = pos >= 0 && pos < p.rope_rows;
 
   if (is_q || is_k) {
     // ---- sum of squares, bit-identical to the left-to-right double sum --------------------------
@@ -101,13 +107,13 @@ qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
       ss = wave_sum(part);  // exact in any order
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) stage[wave][4 * lane + e] = x[e];
+      for (int e = 0; e < 4; ++e) stage[4 * lane + e] = x[e];
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       double seq = 0.0;
       if (lane == 0) {
         for (int i = 0; i < kHeadDim; ++i) {
-          const double v = double(stage[wave][i]);
+          const double v = double(stage[i]);
           seq = seq + v * v;
         }
       }
@@ -126,10 +132,6 @@ qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) partner[e] = __shfl_xor(x[e], 8, 64);
     if (lane < 16 && pos_ok) {
-      const int i0 = 4 * (lane & 7);
-      const float* cs = p.rope + size_t(pos) * kRotaryDim;
-      const float4 c4 = *reinterpret_cast<const float4*>(cs + i0);
-      const float4 s4 = *reinterpret_cast<const float4*>(cs + 32 + i0);
       const float c[4] = {c4.x, c4.y, c4.z, c4.w}, s[4] = {s4.x, s4.y, s4.z, s4.w};
       if (lane < 8) {
 #pragma unroll
@@ -153,10 +155,7 @@ qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
   }
 
   const int head = is_k ? r - p.nq : r - p.nq - p.nkv;
-  const int slot = batch.seq_slot[batch.tok_seq[m]];
-  const int page_idx = pos / kPageTokens;
-  if (!pos_ok || page_idx >= kv.max_pages_per_seq) return;
-  const int page = kv.block_table[size_t(slot) * kv.max_pages_per_seq + page_idx];
+  if (!store_ok) return;
   const int tok = pos % kPageTokens;
   uint8_t* base = kv.pool + size_t(p.attn_layer) * kv.layer_stride + size_t(page) * kv.page_bytes;
   const size_t row = is_k ? kv.layout.k_row(head, tok) : kv.layout.v_row(head, tok);
@@ -189,6 +188,52 @@ qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
   }
 }
 
+// kRows consecutive jobs (token-major rows) per wave: with one row per wave, a large launch is a
+// sequence of rounds of resident waves, each waiting out its own dependent-load chain.
+template <int kRows>
+__global__ void __launch_bounds__(kWavesPerBlock * 64)
+qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
+  __shared__ float stage[kWavesPerBlock][kHeadDim];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int job0 = (blockIdx.x * kWavesPerBlock + wave) * kRows;
+  if (job0 >= jobs) return;
+  const int rows = p.nq + 2 * p.nkv;
+  RowLoads L[kRows];
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    const int job = min(job0 + j, jobs - 1);
+    L[j].m = job / rows;
+    L[j].r = job % rows;
+    const bool is_q = L[j].r < p.nq;
+    // q head r at column r*256; k head h at (2nq + h)*256; v head h at (2nq + nkv + h)*256
+    const int col = (is_q ? L[j].r : p.nq + L[j].r) * kHeadDim;
+    L[j].pos = batch.tok_pos[L[j].m];
+    L[j].raw = *reinterpret_cast<const uint2*>(p.proj + size_t(L[j].m) * p.ld_proj + col + 4 * lane);
+  }
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    const int pos = L[j].pos;
+    const bool pos_ok = pos >= 0 && pos < p.rope_rows;
+    L[j].c4 = float4{1.f, 1.f, 1.f, 1.f};
+    L[j].s4 = float4{0.f, 0.f, 0.f, 0.f};
+    if (L[j].r < p.nq + p.nkv && lane < 16 && pos_ok) {  // q and k rows: cos/sin of this lane's dims
+      const float* cs = p.rope + size_t(pos) * kRotaryDim + 4 * (lane & 7);
+      L[j].c4 = *reinterpret_cast<const float4*>(cs);
+      L[j].s4 = *reinterpret_cast<const float4*>(cs + 32);
+    }
+    const int page_idx = pos / kPageTokens;
+    L[j].store_ok = L[j].r >= p.nq && pos_ok && page_idx < kv.max_pages_per_seq;
+    L[j].page = 0;
+    if (L[j].store_ok) {
+      const int slot = batch.seq_slot[batch.tok_seq[L[j].m]];
+      L[j].page = kv.block_table[size_t(slot) * kv.max_pages_per_seq + page_idx];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kRows; ++j)
+    if (job0 + j < jobs) append_row(p, kv, stage[wave], lane, L[j]);
+}
+
 }  // namespace
 
 int launch_qk_norm_rope_append(const q38a_qk_norm_rope_params& p, const q38a_batch_desc& b,
@@ -199,9 +244,16 @@ int launch_qk_norm_rope_append(const q38a_qk_norm_rope_params& p, const q38a_bat
   if (jobs > (1ll << 30)) return set_error(Q38A_ERR_INVALID, "qk_norm_rope_append: too many tokens (%d)", b.num_tokens);
   AppendArgs a{p.proj, p.ld_proj, p.q_norm, p.k_norm, p.eps, p.num_q_heads, p.num_kv_heads, p.q_out,
                p.attn_layer, p.rope_cos_sin, p.rope_rows};
-  const int blocks = int((jobs + kWavesPerBlock - 1) / kWavesPerBlock);
-  hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(blocks), dim3(kWavesPerBlock * 64), 0, stream, a,
-                     to_args(b), to_args(kv), int(jobs));
+  // four rows per wave for long chunks (2,048 tokens: 49.6 -> 45.2 us; at 519 tokens it was 7% slower)
+  if (jobs > 32768) {
+    const int blocks = int((jobs + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock));
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel<4>, dim3(blocks), dim3(kWavesPerBlock * 64), 0, stream, a,
+                       to_args(b), to_args(kv), int(jobs));
+  } else {
+    const int blocks = int((jobs + kWavesPerBlock - 1) / kWavesPerBlock);
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel<1>, dim3(blocks), dim3(kWavesPerBlock * 64), 0, stream, a,
+                       to_args(b), to_args(kv), int(jobs));
+  }
   return check_hip(hipGetLastError(), "qk_norm_rope_append launch");
 }
 
