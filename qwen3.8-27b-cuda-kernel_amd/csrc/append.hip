@@ -16,8 +16,9 @@
 //
 // Sum of squares: the reference sums x_i^2 in double, left to right. x is bf16, so every x_i^2 is
 // exact in double; the sum is exact in any order whenever the nonzero magnitudes span at most 14
-// binades (24 + 2 * 14 <= 53 bits). The kernel checks that span (wave-wide min/max exponent) and
-// then uses a tree reduction; otherwise one lane replays the left-to-right double sum from LDS.
+// binades (24 + 2 * 14 <= 53 bits), or whenever the total and the lowest set bit of the squares fit
+// in 53 bits. The kernel checks both (wave reductions) and then uses a tree reduction; otherwise
+// one lane replays the left-to-right double sum from LDS.
 #include "common.hpp"
 
 // No multiply-add fusion anywhere in this file: every product and sum rounds on its own, as in the
@@ -42,6 +43,18 @@ constexpr int kWavesPerBlock = 4;
 __device__ inline int exponent_of(float x) {  // floor(log2|x|) for normal x; -149 for subnormals
   const uint32_t e = (as_u32(x) >> 23) & 0xffu;
   return e == 0 ? -149 : int(e) - 127;
+}
+
+// Position of the lowest set bit of a nonzero float: x = odd * 2^lowest_bit_of(x).
+__device__ inline int lowest_bit_of(float x) {
+  const uint32_t b = as_u32(x) & 0x7fffffffu;
+  const uint32_t e = b >> 23, m = b & 0x7fffffu;
+  return e == 0 ? -149 + __builtin_ctz(m) : int(e) - 150 + __builtin_ctz(m | 0x800000u);
+}
+
+// floor(log2 x) for a positive normal double
+__device__ inline int exponent_of_f64(double x) {
+  return int((__builtin_bit_cast(uint64_t, x) >> 52) & 0x7ff) - 1023;
 }
 
 __device__ inline double wave_sum(double v) {
@@ -86,7 +99,7 @@ __device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, float* 
 
   if (is_q || is_k) {
     // ---- sum of squares, bit-identical to the left-to-right double sum --------------------------
-    int emin = 1 << 20, emax = -(1 << 20);
+    int emin = 1 << 20, emax = -(1 << 20), lmin = 1 << 20;
     double part = 0.0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -95,16 +108,23 @@ __device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, float* 
         const int ex = exponent_of(x[e]);
         emin = min(emin, ex);
         emax = max(emax, ex);
+        lmin = min(lmin, lowest_bit_of(x[e]));
       }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       emin = min(emin, __shfl_xor(emin, off, 64));
       emax = max(emax, __shfl_xor(emax, off, 64));
+      lmin = min(lmin, __shfl_xor(lmin, off, 64));
     }
+    // The tree sum equals the left-to-right sum when every partial sum of either order is exact:
+    // (a) the nonzero magnitudes span at most 14 binades, or (b) all partial sums, multiples of
+    // 2^(2 lmin) no larger than the total (< 2^(H + 1)), fit in 53 bits: H + 1 - 2 lmin <= 53. H
+    // comes from the tree sum itself, with one bit of margin for its own rounding.
+    const double tree = wave_sum(part);
     double ss;
-    if (emax - emin <= 14) {
-      ss = wave_sum(part);  // exact in any order
+    if (emax - emin <= 14 || (tree > 0.0 && exponent_of_f64(tree) + 2 - 2 * lmin <= 53)) {
+      ss = tree;  // exact in any order
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) stage[4 * lane + e] = x[e];
