@@ -7,8 +7,8 @@
 // MI355X design. Decode is HBM-bound (each KV byte is used once); with GQA 6 and int8 KV it needs
 // ~12 flop/byte, which at 8 TB/s is more than the non-packed fp32 VALU can issue alongside the
 // int8 widening, so both products run on MFMA and the VALU only widens codes and runs the softmax:
-//   * one workgroup = 4 waves works on one item (sequence, kv head, run of whole pages, see
-//     plan.hpp); each wave takes 16-token blocks of the item's pages in turn;
+//   * one workgroup = 4 waves (8 in the ragged launch) works on one item (sequence, kv head, run of
+//     whole pages, see plan.hpp); each wave takes 16-token blocks of the item's pages in turn;
 //   * S^T[16 tok][16 heads] = K[16 tok][256] . Q^T with v_mfma_f32_16x16x32_f16: K codes enter the
 //     MFMA exactly (int8 -> fp16 by a byte permute and one packed add), Q as stored (fp16), and the
 //     per-(token, 64-dim group) K scale multiplies the four group partials in fp32 afterwards;
@@ -20,7 +20,7 @@
 //     PV product, so probabilities never leave registers;
 //   * K rows are read as 4 x 16-byte loads per lane (a 16-lane group covers 64 contiguous bytes of
 //     a row), V rows as 16 x 4-byte loads (16 lanes cover 64 contiguous bytes);
-//   * the 4 waves' (max, sum, acc) are merged in LDS and written once per item as a partial;
+//   * the waves' (max, sum, acc) are merged in LDS and written once per item as a partial;
 //     attn_merge_kernel combines partials with the log-sum-exp rule and applies sigmoid(gate).
 // bf16 KV pages use the same schedule with bf16 MFMAs for both products; q (fp16) is split exactly
 // into two bf16 operands and P likewise into hi + lo.

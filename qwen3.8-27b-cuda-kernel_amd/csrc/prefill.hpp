@@ -7,9 +7,9 @@
 //
 // MI355X design (one kv head per workgroup, all of its GQA q heads together):
 //   * the q rows of a kv head are the (token, head) pairs of the chunk in token-major order; a
-//     workgroup takes 128 consecutive rows (4 waves x 32 rows), so every K/V tile it stages is
-//     shared by all 6 q heads, and tiles that straddle tokens need no special casing (the causal
-//     limit is per row);
+//     workgroup takes 128 or 256 consecutive rows (4 or 8 waves x 32 rows), so every K/V tile it
+//     stages is shared by all of its rows, and tiles that straddle tokens need no special casing
+//     (the causal limit is per row);
 //   * K/V tiles of 32 keys are read as int8 codes + fp16 scales with coalesced 16-byte loads one
 //     tile ahead, dequantised (code * scale, rounded once to fp16, exactly like the reference's
 //     fp16 staging) into double-buffered LDS, K and V both as [key][dim]; bf16 pages are converted
@@ -294,9 +294,9 @@ __device__ inline half4_t v_keys4(const KvTile& T, int key0, int dim0, int j) {
 // running max m and sum l in fp32, padded to 528 bytes. Half the bytes of an fp32 accumulator row.
 constexpr int kPartialRowFloats = kHeadDim / 2 + 4;
 
-// Row tile `tile` of sequence b and kv head kvh, key blocks [part * kt / parts, (part + 1) * kt / parts)
+// Row tile `tile` (32 kWavesWG rows) of sequence b and kv head kvh, key blocks [part * kt / parts, (part + 1) * kt / parts)
 // of the tile's kt = ceil(kend / 32) blocks. With parts == 1 the result is final (normalised, gated,
-// bf16 into a.out); otherwise the tile's partial goes to `partial`: [128 rows][kPartialRowFloats]
+// bf16 into a.out); otherwise the tile's partial goes to `partial`: [rows][kPartialRowFloats]
 // (O / l in fp16, then m, l per row in the exp2 domain; m = -inf and l = 0 for a row without keys).
 template <int DT, bool kLookahead = false, int kWavesWG = kPWaves>
 __device__ __attribute__((always_inline)) inline void prefill_unit(const PrefillArgs& a, const BatchArgs& batch,
