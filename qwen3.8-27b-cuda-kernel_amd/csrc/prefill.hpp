@@ -437,7 +437,9 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
     // O^T += V^T . P^T: MFMA step t covers keys 16 t + {0..3, 8..11} (k-group 0) and
     // 16 t + {4..7, 12..15} (k-group 1), matching where P^T already sits
     if constexpr (kLookahead) {
-      constexpr int kVDepth = 2;  // as for K: reads two MFMAs ahead (two transposing reads each)
+      // as for K, two transposing reads per operand; eight-wave workgroups have the registers for
+      // three operands ahead (config 3 0.476 -> 0.465 ms; four or three K operands: no better)
+      constexpr int kVDepth = kWavesWG == 8 ? 3 : 2;
       auto vread = [&](int i) {  // operand i = 8 t + dt
         const int t = i >> 3, dt = i & 7;
         const int kk = 16 * t + 4 * kg;
