@@ -87,7 +87,7 @@ struct RowLoads {
 };
 
 // One (token, head row): norm, RoPE, then the q store or the page-row store, from its loads.
-__device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, float* stage, int lane, const RowLoads& L) {
+__device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, double* stage, int lane, const RowLoads& L) {
   const int m = L.m, r = L.r, pos = L.pos, page = L.page;
   const bool store_ok = L.store_ok;
   const uint2 raw = L.raw;
@@ -127,7 +127,7 @@ __device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, float* 
       ss = tree;  // exact in any order
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) stage[4 * lane + e] = x[e];
+      for (int e = 0; e < 4; ++e) stage[4 * lane + e] = double(x[e]);  // converted off the serial chain
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       double seq = 0.0;
@@ -135,7 +135,7 @@ __device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, float* 
         // fma(v, v, seq) = fl(seq + v * v) = fl(seq + fl(v * v)): v is a bf16 value, so v * v is exact
         // in double and the single rounding is the reference's; one instruction less per element
         for (int i = 0; i < kHeadDim; ++i) {
-          const double v = double(stage[i]);
+          const double v = stage[i];
           seq = __builtin_fma(v, v, seq);
         }
       }
@@ -215,7 +215,7 @@ __device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, float* 
 template <int kRows>
 __global__ void __launch_bounds__(kWavesPerBlock * 64)
 qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
-  __shared__ float stage[kWavesPerBlock][kHeadDim];
+  __shared__ double stage[kWavesPerBlock][kHeadDim];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int job0 = (blockIdx.x * kWavesPerBlock + wave) * kRows;
   if (job0 >= jobs) return;
