@@ -51,6 +51,9 @@ struct DecodeArgs {
   // the CUs (the ragged launch's prefill units), at the price of run-to-run bit reproducibility:
   // which wave sums which block changes the fp32 summation order. Off: a fixed schedule.
   bool dynamic_claims;
+  // Items handed out by a launch-wide counter (g_item_queue) instead of a fixed stride: workgroups
+  // that start late (behind other work on their CUs) take fewer items.
+  bool item_queue;
 };
 
 
@@ -431,6 +434,7 @@ struct alignas(16) WaveMerge {
 template <int W = kWaves>
 struct alignas(16) DecodeShared {
   WaveMerge<W> merge;  // the W waves' state at the end of an item
+  int next_item;       // the item the workgroup takes next (item queue)
 };
 
 // Merges the W waves' (m, l, O) of an item in LDS and writes the item's partial to scratch.
@@ -488,6 +492,10 @@ constexpr int kTeam = 8;            // workgroups (splits) per team: consecutive
 constexpr int kClaimSlots = 4096;   // teams whose first item index is larger use the static schedule
 constexpr int kClaimStride = 32;    // ints per slot
 __device__ int g_claims[kClaimSlots * kClaimStride];
+// The item queue: the next item of the launch. Each of the launch's nwg decode workgroups takes
+// items until it draws one past the last (pl.items); those draws are pl.items .. pl.items + nwg - 1,
+// and the last of them resets the counter for the next launch (same one-stream rule as the claims).
+__device__ int g_item_queue[kClaimStride];
 
 // Persistent loop over the decode items of a launch: this workgroup is number `wg` of `nwg` that
 // stride over items of pl.cp pages (wave_decode_plan). The items of a decode row are ordered
@@ -501,7 +509,18 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
                                                                    DecodeShared<W>& sh, int wg, int nwg) {
   const int cp = pl.cp;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  for (int item = wg;; item += nwg) {
+  // sh.next_item is written before the first barrier of the grab and read after it; the previous
+  // item's finish_item ends with a barrier, so no wave still reads the old value
+  auto grab = [&]() {
+    if (threadIdx.x == 0) {
+      const int c = __hip_atomic_fetch_add(&g_item_queue[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (c == pl.items + nwg - 1) __hip_atomic_store(&g_item_queue[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sh.next_item = c;
+    }
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(sh.next_item);
+  };
+  for (int item = a.item_queue ? grab() : wg;; item = a.item_queue ? grab() : item + nwg) {
     const ItemSpot at = wave_locate(batch, a.nkv, pl, item);
     if (at.seq < 0) break;
     const int b = at.seq;

@@ -107,6 +107,7 @@ __device__ inline int wave_max_i(int x) {
 struct DecodePlan {
   int cp;      // pages per item (wave-uniform)
   int pages0;  // pages of decode row `lane` (rows 0..63), kept so locating items rereads nothing
+  int items;   // decode items of the launch (wave-uniform)
 };
 
 __device__ inline int decode_pages(const BatchArgs& batch, int s) {
@@ -130,6 +131,9 @@ __device__ inline DecodePlan wave_decode_plan(const BatchArgs& batch, int nkv, i
   const int by_splits = ceil_div_i(pmax, max_splits);
   const int by_target = int((static_cast<long long>(psum) * nkv + target_items - 1) / target_items);
   pl.cp = __builtin_amdgcn_readfirstlane(max(1, max(by_splits, by_target)));
+  int items = ceil_div_i(pl.pages0, pl.cp);
+  for (int s0 = 64; s0 < batch.num_seqs; s0 += 64) items += ceil_div_i(decode_pages(batch, s0 + lane), pl.cp);
+  pl.items = __builtin_amdgcn_readfirstlane(wave_sum_i(items) * nkv);
   return pl;
 }
 

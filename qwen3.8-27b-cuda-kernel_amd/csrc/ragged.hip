@@ -6,13 +6,14 @@
 // decode rows and attention_prefill (src/kernels/attention_prefill.cu:154-313) for the chunks; the
 // reference runs them as separate launches (src/engine.cpp:133-182).
 //
-// Launch layout: grid = P prefill workgroups followed by D = CUs decode workgroups, all eight waves
-// (512 threads) with the same register and LDS budget (one workgroup per CU), so both kinds share
-// the CUs. Eight waves let a prefill unit stage each key tile once for 256 rows (half the staging
+// Launch layout: grid = F decode workgroups, P prefill workgroups, then CUs - F more decode
+// workgroups (F = CUs / 8 when the batch has a prefill chunk, else 0), all eight waves (512 threads)
+// with the same register and LDS budget (one workgroup per CU), so both kinds share the CUs. Eight waves let a prefill unit stage each key tile once for 256 rows (half the staging
 // per thread of four-wave units, the registers for the operand lookahead) and a decode item spread
-// over eight waves. Workgroups are
-// dispatched in index order, so the long prefill units start first and the short, HBM-bound decode
-// items fill in behind them.
+// over eight waves. Workgroups are dispatched in index order: the first F decode workgroups stream
+// decode pages from their CUs while the prefill units (aimed at the other CUs) keep the MFMA busy,
+// and the later decode workgroups take the remaining decode items (a launch-wide item queue) as
+// prefill units finish.
 //   * prefill: every (row tile, kv head) of a chunk is cut into parts of about the same number of key
 //     blocks (plan.hpp build_prefill_plan) so that a 512-token chunk still spreads over the whole
 //     chip; a tile with one part stores its final output, otherwise each part stores an
@@ -30,7 +31,7 @@
 namespace q38a {
 namespace {
 
-constexpr int kPrefillTarget = 256;  // prefill units aimed for per launch (one per CU on MI355X)
+constexpr int kPrefillTarget = 256;  // prefill units aimed for per launch at most (one per CU on MI355X)
 constexpr int kRaggedWaves = 8;
 constexpr int kRaggedThreads = 64 * kRaggedWaves;
 constexpr int kMinChunk = 16;        // key blocks per part at least (512 keys)
@@ -45,6 +46,8 @@ static_assert(kParts + kMaxSeqs <= kHeaderInts, "ragged scratch header");
 
 struct RaggedArgs {
   int prefill_blocks;
+  int decode_first;    // decode workgroups placed before the prefill units (0: after them)
+  int prefill_target;  // prefill units aimed for
   int* header;
   float* prefill_partials;
 };
@@ -64,11 +67,14 @@ __global__ void __launch_bounds__(kRaggedThreads, 1)
     DecodeShared<kRaggedWaves> dec;
   } sh;
   const int B = batch.num_seqs;
-  if (int(blockIdx.x) < r.prefill_blocks) {
+  const int bid = int(blockIdx.x);
+  const bool is_prefill = bid >= r.decode_first && bid < r.decode_first + r.prefill_blocks;
+  if (is_prefill) {
     {
-      build_prefill_plan(batch, pa.group, pa.nkv, kPrefillTarget, kMinChunk, plan);
+      build_prefill_plan(batch, pa.group, pa.nkv, r.prefill_target, kMinChunk, plan);
       const int chunk = plan.chunk_pages;
-      if (blockIdx.x == 0) {  // what the merge needs: parts, unit and merge-task offsets per sequence
+      const int u = bid - r.decode_first;
+      if (u == 0) {  // what the merge needs: parts, unit and merge-task offsets per sequence
         int tasks[kPlanPer];
 #pragma unroll
         for (int i = 0; i < kPlanPer; ++i) {
@@ -81,7 +87,6 @@ __global__ void __launch_bounds__(kRaggedThreads, 1)
         if (threadIdx.x == 0) r.header[1] = chunk;
         block_scan_store(tasks, B, r.header + kTaskPrefix, plan);
       }
-      const int u = blockIdx.x;
       if (u >= plan.prefix[B]) return;
       const int b = __builtin_amdgcn_readfirstlane(find_seq(plan, B, u));
       const int local = u - plan.prefix[b];
@@ -95,7 +100,7 @@ __global__ void __launch_bounds__(kRaggedThreads, 1)
     }
   } else {
     const DecodePlan pl = wave_decode_plan(batch, d.nkv, d.max_splits, d.target_items);
-    const int wg = int(blockIdx.x) - r.prefill_blocks;
+    const int wg = bid < r.decode_first ? bid : bid - r.prefill_blocks;
     if (wg == 0 && threadIdx.x == 0) r.header[0] = pl.cp;
     decode_items<DT, kRaggedWaves>(d, batch, kv, pl, sh.dec, wg, int(gridDim.x) - r.prefill_blocks);
   }
@@ -193,14 +198,20 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   if (int rc = device_cu_count(&cus)) return rc;
   // one eight-wave decode workgroup per CU, two items each (one item per workgroup: 54 vs 49 us for
   // config 4's decode rows alone; three: 55)
-  const int dgrid = cus, target = 2 * cus;
+  // With prefill chunks in the batch, cus / 8 decode workgroups (4 per XCD) come first and stream
+  // the decode rows' pages beside the MFMA-bound prefill units, which aim at the other CUs; the rest
+  // follow the prefill units and join the item queue as CUs free up. Config 4: 187 -> 174 us (16,
+  // 24, 40 and 48 first: 177, 176, 179, 178); a decode-heavy mix (a 128-token chunk + 15 rows of
+  // 30-44K): 261 -> 250 us.
+  const int dfirst = b.max_tokens_per_seq > 1 ? cus / 8 : 0;
+  const int dgrid = cus, target = 2 * dgrid;
   int* header = reinterpret_cast<int*>(p.split_scratch);
   float* dec = p.split_scratch + kHeaderInts;
   float* pre = dec + s.decode_floats;
   const int pblocks = int(s.units_bound);
-  RaggedArgs r{pblocks, header, pre};
+  RaggedArgs r{pblocks, dfirst, min(kPrefillTarget, cus - dfirst), header, pre};
   DecodeArgs d{p.q, p.num_q_heads, p.num_kv_heads, G, p.attn_layer, dec, p.max_splits, target, p.gate, p.ld_gate,
-               p.out, true};
+               p.out, true, true};
   PrefillArgs pa{p.q, p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, p.attn_layer};
   const dim3 grid(unsigned(pblocks + dgrid));
   if (kv.dtype == Q38A_KV_INT8)
