@@ -108,3 +108,14 @@ def test_ragged_config3_through_ragged(orc):
     """Config 3 (2048-token chunk on a 6000-token prefix) through the ragged launch: tiles split."""
     toks = sorted(set([0, 1, 47, 48, 1000, 2046, 2047] + list(range(5, 2048, 97))))
     ragged_step(orc, [(6000, 2048)], seed=3, check_tokens=[toks], compare_split_launches=True)
+
+
+def test_ragged_back_to_back_launches(orc):
+    """Launches of different shapes in a row (with and without prefill chunks, so with and without
+    decode workgroups placed before the prefill units): the launch-wide decode item queue and the
+    block-claim counters must start every launch at zero, which the previous launch's last draw
+    restores."""
+    mixed = [(3000, 40), (9000, 1), (700, 1), (15000, 1), (64, 1)]
+    decode = [(c, 1) for c in (4000, 129, 20000, 640)]
+    for i, seqs in enumerate([mixed, decode, mixed, decode, [(6000, 300)], mixed]):
+        ragged_step(orc, seqs, seed=40 + i)
