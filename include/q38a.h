@@ -159,7 +159,8 @@ size_t q38a_ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_p
  * applied to each sequence. The decode rows' key blocks are handed out dynamically, so their
  * fp32 summation order, and rarely a last bf16 bit, can differ from run to run (decode and
  * prefill launches are bit-reproducible). Launches on one device must not overlap in time
- * (they share the block-claim counters): keep them on one stream. */
+ * (they share the decode item queue and block-claim counters, static device memory): keep them
+ * on one stream. */
 int q38a_attention_ragged(const q38a_attention_params* p, const q38a_batch_desc* batch,
                           const q38a_kv_cache_desc* kv, void* stream);
 
