@@ -632,15 +632,16 @@ __device__ inline void merge_row(const float* src, int splits, size_t stride, co
 
 // merge_row for prefill partial rows (kPartialRowFloats: O / l in fp16, then m, l): split s weighs
 // 2^(m_s - M) l_s. One wave; lane l owns dims 4l + [0, 4).
-__device__ inline void merge_row_h16(const float* src, int splits, size_t stride, const uint16_t* gate_row,
-                                     uint16_t* out_row) {
+template <int kBatch>
+__device__ inline void merge_row_h16_b(const float* src, int splits, size_t stride, const uint16_t* gate_row,
+                                       uint16_t* out_row) {
   const int d = 4 * (threadIdx.x & 63);
   float M = -INFINITY, wsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
-    uint2 v[kMergeBatch];
-    float2 ml[kMergeBatch];
+  for (int s0 = 0; s0 < splits; s0 += kBatch) {
+    uint2 v[kBatch];
+    float2 ml[kBatch];
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const int s = min(s0 + u, splits - 1);
       const float* p = src + s * stride;
       v[u] = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + d);
@@ -649,7 +650,7 @@ __device__ inline void merge_row_h16(const float* src, int splits, size_t stride
     }
     float bm = M;
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) bm = fmaxf(bm, ml[u].x);
+    for (int u = 0; u < kBatch; ++u) bm = fmaxf(bm, ml[u].x);
     if (bm == -INFINITY) continue;  // uniform
     const float c = __builtin_amdgcn_exp2f(M - bm);
     M = bm;
@@ -657,7 +658,7 @@ __device__ inline void merge_row_h16(const float* src, int splits, size_t stride
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] *= c;
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const float w = __builtin_amdgcn_exp2f(ml[u].x - M) * ml[u].y;  // empty split: 0
       const half2_t a = __builtin_bit_cast(half2_t, v[u].x), b = __builtin_bit_cast(half2_t, v[u].y);
       wsum += w;
@@ -673,6 +674,15 @@ __device__ inline void merge_row_h16(const float* src, int splits, size_t stride
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = bf16_bits((wsum > 0.f ? acc[i] / wsum : 0.f) * sigmoid_gate(gv[i]));
   *reinterpret_cast<uint2*>(out_row + d) = uint2{uint32_t(o[0]) | (uint32_t(o[1]) << 16), uint32_t(o[2]) | (uint32_t(o[3]) << 16)};
+}
+
+// The split loads of one batch are issued together; the batch follows the split count so that a
+// row with few splits does not issue (clamped, repeated) loads for splits it does not have.
+__device__ inline void merge_row_h16(const float* src, int splits, size_t stride, const uint16_t* gate_row,
+                                     uint16_t* out_row) {
+  if (splits <= 4) merge_row_h16_b<4>(src, splits, stride, gate_row, out_row);
+  else if (splits <= 8) merge_row_h16_b<8>(src, splits, stride, gate_row, out_row);
+  else merge_row_h16_b<kMergeBatch>(src, splits, stride, gate_row, out_row);
 }
 
 struct alignas(16) MergeShared {
