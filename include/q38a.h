@@ -151,6 +151,11 @@ int q38a_attention_prefill(const q38a_attention_params* p, const q38a_batch_desc
 size_t q38a_ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int num_q_heads,
                                   int num_kv_heads, int max_splits);
 
+/* Zeroes the counters at the front of a ragged scratch buffer (asynchronous on `stream`). Call it
+ * once after allocating the buffer, unless it was allocated zeroed; every q38a_attention_ragged
+ * launch leaves the counters zero again. No counterpart in the reference. */
+int q38a_ragged_scratch_init(float* split_scratch, void* stream);
+
 /* Mixed continuous-batching step: sequences with one token (decode rows) and with several
  * (prefill chunks) in one ragged batch, scheduled by one attention launch plus the split merge;
  * split_scratch holds q38a_ragged_scratch_floats(...) floats.
@@ -158,9 +163,10 @@ size_t q38a_ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_p
  * decode as separate launches); semantics are those of attention_decode / attention_prefill
  * applied to each sequence. The decode rows' key blocks are handed out dynamically, so their
  * fp32 summation order, and rarely a last bf16 bit, can differ from run to run (decode and
- * prefill launches are bit-reproducible). Launches on one device must not overlap in time
- * (they share the decode item queue and block-claim counters, static device memory): keep them
- * on one stream. */
+ * prefill launches are bit-reproducible). The launch's work counters (decode item queue and
+ * block claims) live at the front of split_scratch: launches with separate scratch buffers are
+ * independent and may run concurrently on different streams; one scratch buffer serves one
+ * launch at a time. */
 int q38a_attention_ragged(const q38a_attention_params* p, const q38a_batch_desc* batch,
                           const q38a_kv_cache_desc* kv, void* stream);
 

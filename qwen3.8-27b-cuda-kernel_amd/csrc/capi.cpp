@@ -19,6 +19,7 @@ int launch_attention_prefill(const q38a_attention_params& p, const q38a_batch_de
                              const q38a_kv_cache_desc& kv, hipStream_t stream);
 int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
                             hipStream_t stream);
+int ragged_scratch_init(float* scratch, hipStream_t stream);
 int max_group();
 size_t ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits);
 
@@ -221,6 +222,12 @@ int q38a_attention_prefill(const q38a_attention_params* p, const q38a_batch_desc
   clear_error();
   if (int rc = validate_attention(p, batch, kv, false)) return rc;
   return launch_attention_prefill(*p, *batch, *kv, static_cast<hipStream_t>(stream));
+}
+
+int q38a_ragged_scratch_init(float* split_scratch, void* stream) {
+  clear_error();
+  if (!split_scratch) return set_error(Q38A_ERR_INVALID, "ragged_scratch_init: scratch is null");
+  return ragged_scratch_init(split_scratch, static_cast<hipStream_t>(stream));
 }
 
 int q38a_attention_ragged(const q38a_attention_params* p, const q38a_batch_desc* batch,

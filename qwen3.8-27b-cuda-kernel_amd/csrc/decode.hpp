@@ -36,6 +36,9 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxGroup = 8;
 constexpr int kMaxMergeSplits = 512;  // max_splits accepted by the launchers
+constexpr int kTeam = 8;            // workgroups (splits) per claim team: consecutive ones sit on 8 XCDs
+constexpr int kClaimSlots = 4096;   // teams whose first item index is larger use the static schedule
+constexpr int kClaimStride = 32;    // ints per counter (one 128-byte line)
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -51,9 +54,13 @@ struct DecodeArgs {
   // the CUs (the ragged launch's prefill units), at the price of run-to-run bit reproducibility:
   // which wave sums which block changes the fp32 summation order. Off: a fixed schedule.
   bool dynamic_claims;
-  // Items handed out by a launch-wide counter (g_item_queue) instead of a fixed stride: workgroups
+  // Items handed out by a launch-wide counter (*queue) instead of a fixed stride: workgroups
   // that start late (behind other work on their CUs) take fewer items.
   bool item_queue;
+  // Counters of the two dynamic schedules, in the caller's scratch (one 128-byte line each); they
+  // must be zero when the launch starts, and the launch's merge kernel zeroes them again.
+  int* claims;  // [kClaimSlots][kClaimStride]
+  int* queue;
 };
 
 
@@ -248,14 +255,6 @@ struct BlockSource {
   int* ctr;     // dynamic: the team's claim counter
 };
 
-// A team's counter ends a launch at (successful claims) + (one failing claim per wave that had a
-// first block); the wave whose failing claim returns the last value resets it, so every launch
-// finds it at zero.
-__device__ inline bool last_claim(const BlockSource& src, int c) {
-  const int waves = min(src.base, src.nblk);
-  return c == max(0, src.nblk - src.base) + waves - 1;
-}
-
 // int8 pages: the blocks of `src`; the next block's loads are in flight while the current one is
 // computed, and with a claim counter the claim after that is in flight too. Block indices, pages
 // and block-table reads are wave-uniform; blocks past te are masked. The waves of a workgroup do
@@ -312,8 +311,6 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
     const int c = __builtin_amdgcn_readfirstlane(pending);
     const int nidx = dynamic ? src.base + c : idx + src.stride;
     const bool more = nidx < src.nblk;  // uniform
-    if (dynamic && !more && last_claim(src, c) && lane == 0)
-      __hip_atomic_store(src.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (more && dynamic) pending = claim();
     // unconditional (the last iteration reloads the current block): with a single path the
     // compiler's wait for the current block does not also cover the next block's loads
@@ -483,19 +480,11 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge<W>& sm, int b, int kv
   __syncthreads();
 }
 
-// Claim counters of the dynamic block schedule, one per team of up to kTeam consecutive splits of
-// a (decode row, kv head), in the slot of the team's first item, one 128-byte line each (claims on
-// one line serialise). They start at zero (static storage) and the last claim of a launch resets
-// its counter (last_claim). Launches that overlap in time on one device would share them: run
-// them on one stream.
-constexpr int kTeam = 8;            // workgroups (splits) per team: consecutive ones sit on 8 XCDs
-constexpr int kClaimSlots = 4096;   // teams whose first item index is larger use the static schedule
-constexpr int kClaimStride = 32;    // ints per slot
-__device__ int g_claims[kClaimSlots * kClaimStride];
-// The item queue: the next item of the launch. Each of the launch's nwg decode workgroups takes
-// items until it draws one past the last (pl.items); those draws are pl.items .. pl.items + nwg - 1,
-// and the last of them resets the counter for the next launch (same one-stream rule as the claims).
-__device__ int g_item_queue[kClaimStride];
+// Claim counters of the dynamic block schedule (DecodeArgs::claims), one per team of up to kTeam
+// consecutive splits of a (decode row, kv head), in the slot of the team's first item, one 128-byte
+// line each (claims on one line serialise). The item queue (DecodeArgs::queue) holds the next item
+// of the launch. Both live in the caller's scratch, so launches with their own scratch never
+// interact; the merge kernel that follows a launch zeroes every counter the launch used.
 
 // Persistent loop over the decode items of a launch: this workgroup is number `wg` of `nwg` that
 // stride over items of pl.cp pages (wave_decode_plan). The items of a decode row are ordered
@@ -513,9 +502,7 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
   // item's finish_item ends with a barrier, so no wave still reads the old value
   auto grab = [&]() {
     if (threadIdx.x == 0) {
-      const int c = __hip_atomic_fetch_add(&g_item_queue[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (c == pl.items + nwg - 1) __hip_atomic_store(&g_item_queue[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sh.next_item = c;
+      sh.next_item = __hip_atomic_fetch_add(a.queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     return __builtin_amdgcn_readfirstlane(sh.next_item);
@@ -544,7 +531,7 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
         src.te = min(L, src.tb + members * span);
         src.first = member * W + wave;
         src.base = members * W;
-        src.ctr = &g_claims[slot * kClaimStride];
+        src.ctr = a.claims + size_t(slot) * kClaimStride;
       } else {
         src.tb = split * span;
         src.te = min(L, src.tb + span);

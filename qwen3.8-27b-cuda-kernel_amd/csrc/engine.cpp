@@ -3,9 +3,10 @@
 // number of tokens to generate; "sampling" a token only advances the sequence, because the
 // attention step is all this library runs.
 //
-//   * admission (reference :62-91): requests are admitted in order while a slot is free; the pages
-//     of the whole request, min(prompt + max_new, max_context) tokens, are reserved up front so no
-//     sequence is ever preempted; a request that cannot fit even in an empty engine fails;
+//   * admission (same contract as reference :62-91): requests start in arrival order; the pages of
+//     the whole request, min(prompt + max_new, max_context) tokens, are reserved when it starts,
+//     so no sequence is ever preempted; a request that could not run even alone is refused (here
+//     as soon as it reaches the head of the queue, rather than after the engine has drained);
 //   * one iteration = at most one prefill chunk (the oldest sequence still consuming its prompt)
 //     plus one decode row for every sequence that has a sampled token not yet in the cache;
 //   * policy 0 (reference :133-182): the chunk runs as its own prefill launch, then one decode
@@ -81,36 +82,43 @@ bool on_sample(q38a_engine* e, Sequence& s) {
   return false;
 }
 
+// Pages a request holds from admission to its end: its prompt plus every token it may generate,
+// capped by the context limit.
+int footprint_pages(const q38a_engine* e, const Sequence& s) {
+  const long long tokens = std::min<long long>(static_cast<long long>(s.prompt) + s.max_new, e->max_context);
+  return int((tokens + kPageTokens - 1) / kPageTokens);
+}
+
+// Pages that are free now or held by running sequences, i.e. free once every one of them ends.
+int reclaimable_pages(q38a_engine* e) {
+  q38a_kv_cache* kv = q38a_runner_kv(e->runner);
+  int pages = q38a_kv_cache_free_pages(kv);
+  for (const Sequence& s : e->active) pages += q38a_kv_cache_pages_of(kv, s.slot);
+  return pages;
+}
+
+// Moves requests from the head of the queue into `active`, strictly in arrival order. A request is
+// refused outright when it can never run (its prompt reaches the context limit, or its footprint
+// exceeds what the pool holds even with nothing else running); the head request otherwise waits
+// until a slot and its whole footprint are free, and nothing behind it overtakes it.
 int admit(q38a_engine* e) {
   q38a_kv_cache* kv = q38a_runner_kv(e->runner);
-  while (!e->waiting.empty() && !e->free_slots.empty()) {
-    Sequence& s = e->waiting.front();
-    if (s.prompt >= e->max_context) {
-      Sequence f = s;
+  while (!e->waiting.empty()) {
+    Sequence head = e->waiting.front();
+    const int pages = footprint_pages(e, head);
+    if (head.prompt >= e->max_context || pages > reclaimable_pages(e)) {
       e->waiting.pop_front();
-      finish(e, f, true);
+      finish(e, head, true);
       continue;
     }
-    const int want = int(std::min<long long>(static_cast<long long>(s.prompt) + s.max_new, e->max_context));
-    const int slot = e->free_slots.back();
-    int ok = 0;
-    if (int rc = q38a_kv_cache_ensure(kv, slot, want, &ok)) {
-      if (rc != Q38A_ERR_CAPACITY) return rc;
-      ok = 0;
-    }
-    if (!ok) {
-      if (e->active.empty()) {  // cannot fit even alone
-        Sequence f = s;
-        e->waiting.pop_front();
-        finish(e, f, true);
-        continue;
-      }
-      break;  // wait for running sequences to free pages
-    }
+    if (e->free_slots.empty() || pages > q38a_kv_cache_free_pages(kv)) break;
+    head.slot = e->free_slots.back();
+    int granted = 0;
+    if (int rc = q38a_kv_cache_ensure(kv, head.slot, pages * kPageTokens, &granted)) return rc;
+    if (!granted) return set_error(Q38A_ERR_CAPACITY, "engine: %d free pages did not cover %d", q38a_kv_cache_free_pages(kv), pages);
     e->free_slots.pop_back();
-    s.slot = slot;
-    e->active.push_back(s);
     e->waiting.pop_front();
+    e->active.push_back(head);
   }
   return Q38A_OK;
 }
@@ -249,7 +257,7 @@ int q38a_engine_execute(q38a_engine* e, void* stream) {
   for (int i : e->rows) {
     Sequence& s = e->active[size_t(i)];
     if (gone[size_t(i)]) continue;
-    s.position += 1;  // the pending token is now in the cache
+    s.position += 1;  // this step appended the row's token at its position
     ++e->stats.decode_tokens;
     if (on_sample(e, s)) gone[size_t(i)] = 1;
   }

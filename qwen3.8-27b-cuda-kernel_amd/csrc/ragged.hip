@@ -23,8 +23,11 @@
 // The plan is recomputed on the device from seq_start / seq_pos0 (graph-capturable); the first
 // workgroup of each kind records what the merge needs in the scratch header.
 //
-// Scratch (floats, q38a_ragged_scratch_floats): header (kHeaderInts ints) | decode partials
-// [B][nq][max_splits][258] | prefill partials [units][256 rows][kPartialRowFloats].
+// Scratch (floats, q38a_ragged_scratch_floats): header (kHeaderInts ints) | claim counters
+// (kClaimSlots lines of 128 bytes) | decode partials [B][nq][max_splits][258] | prefill partials
+// [units][256 rows][kPartialRowFloats]. The header's queue counter and the claim counters must be
+// zero before a scratch buffer's first launch (allocate it zeroed); every launch's merge kernel
+// zeroes them again, so launches are independent of each other and of any other scratch buffer.
 #include "decode.hpp"
 #include "prefill.hpp"
 
@@ -36,13 +39,16 @@ constexpr int kRaggedWaves = 8;
 constexpr int kRaggedThreads = 64 * kRaggedWaves;
 constexpr int kMinChunk = 16;        // key blocks per part at least (512 keys)
 constexpr int kHeaderInts = 4096;
-// header: [0] decode pages per item, [1] prefill key blocks per part,
+// header: [0] decode pages per item, [1] prefill key blocks per part, [2] decode items,
 //         [kTaskPrefix + b] merge tasks (split tile, kv head) before sequence b,
-//         [kUnitPrefix + b] prefill units before sequence b, [kParts + b] parts per tile
+//         [kUnitPrefix + b] prefill units before sequence b, [kParts + b] parts per tile,
+//         [kQueue] the decode item queue (a 128-byte line of its own)
 constexpr int kTaskPrefix = 4;
 constexpr int kUnitPrefix = kTaskPrefix + kMaxSeqs + 1;
 constexpr int kParts = kUnitPrefix + kMaxSeqs + 1;
-static_assert(kParts + kMaxSeqs <= kHeaderInts, "ragged scratch header");
+constexpr int kQueue = kHeaderInts - kClaimStride;
+static_assert(kParts + kMaxSeqs <= kQueue, "ragged scratch header");
+constexpr size_t kClaimFloats = size_t(kClaimSlots) * kClaimStride;
 
 struct RaggedArgs {
   int prefill_blocks;
@@ -101,7 +107,10 @@ __global__ void __launch_bounds__(kRaggedThreads, 1)
   } else {
     const DecodePlan pl = wave_decode_plan(batch, d.nkv, d.max_splits, d.target_items);
     const int wg = bid < r.decode_first ? bid : bid - r.prefill_blocks;
-    if (wg == 0 && threadIdx.x == 0) r.header[0] = pl.cp;
+    if (wg == 0 && threadIdx.x == 0) {
+      r.header[0] = pl.cp;
+      r.header[2] = pl.items;
+    }
     decode_items<DT, kRaggedWaves>(d, batch, kv, pl, sh.dec, wg, int(gridDim.x) - r.prefill_blocks);
   }
 }
@@ -115,6 +124,8 @@ struct RaggedMergeArgs {
   const float* decode_partials;
   const float* prefill_partials;
   int max_splits;
+  int* queue;
+  int* claims;
 };
 
 // grid: B * nq decode blocks (a workgroup per decode row and q head), then kPrefillRows / 4 blocks
@@ -123,6 +134,15 @@ __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(Ragged
   __shared__ MergeShared sh;
   const int B = batch.num_seqs;
   const int blk = blockIdx.x;
+  // The attention kernel has finished (same stream): zero the counters it used for the next launch.
+  // Claim slots are indexed by a team's first item, so slots [0, items) cover every used one (the
+  // attention kernel's first decode workgroup recorded the item count).
+  {
+    const int used = min(a.header[2], kClaimSlots);
+    for (int i = blk * kMergeThreads + int(threadIdx.x); i < used; i += int(gridDim.x) * kMergeThreads)
+      a.claims[size_t(i) * kClaimStride] = 0;
+    if (blk == 0 && threadIdx.x == 0) *a.queue = 0;
+  }
   if (blk < B * a.nq) {
     const int b = blk / a.nq, hq = blk % a.nq;
     const int L = decode_len(batch, b);
@@ -182,7 +202,22 @@ RaggedShape ragged_shape(int num_seqs, int num_tokens, int max_tokens_per_seq, i
 
 size_t ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits) {
   const RaggedShape s = ragged_shape(num_seqs, num_tokens, max_tokens_per_seq, nq, nkv, max_splits);
-  return size_t(kHeaderInts) + s.decode_floats + s.units_bound * kPrefillRows * kPartialRowFloats;
+  return size_t(kHeaderInts) + kClaimFloats + s.decode_floats + s.units_bound * kPrefillRows * kPartialRowFloats;
+}
+
+namespace {
+// Zeroes the counter region (header + claim lines) of a ragged scratch buffer: a plain fill kernel,
+// so the call is also safe inside graph capture.
+__global__ void __launch_bounds__(256) ragged_counters_zero_kernel(int* p, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) p[i] = 0;
+}
+}  // namespace
+
+int ragged_scratch_init(float* scratch, hipStream_t stream) {
+  const size_t n = size_t(kHeaderInts) + kClaimFloats;
+  hipLaunchKernelGGL(ragged_counters_zero_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                     reinterpret_cast<int*>(scratch), n);
+  return check_hip(hipGetLastError(), "ragged_scratch_init launch");
 }
 
 int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
@@ -206,12 +241,13 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   const int dfirst = b.max_tokens_per_seq > 1 ? cus / 8 : 0;
   const int dgrid = cus, target = 2 * dgrid;
   int* header = reinterpret_cast<int*>(p.split_scratch);
-  float* dec = p.split_scratch + kHeaderInts;
+  int* claims = header + kHeaderInts;
+  float* dec = p.split_scratch + kHeaderInts + kClaimFloats;
   float* pre = dec + s.decode_floats;
   const int pblocks = int(s.units_bound);
   RaggedArgs r{pblocks, dfirst, min(kPrefillTarget, cus - dfirst), header, pre};
   DecodeArgs d{p.q, p.num_q_heads, p.num_kv_heads, G, p.attn_layer, dec, p.max_splits, target, p.gate, p.ld_gate,
-               p.out, true, true};
+               p.out, true, true, claims, header + kQueue};
   PrefillArgs pa{p.q, p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, p.attn_layer};
   const dim3 grid(unsigned(pblocks + dgrid));
   if (kv.dtype == Q38A_KV_INT8)
@@ -221,7 +257,8 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
     hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_BF16>, grid, dim3(kRaggedThreads), 0, stream, r, d, pa, to_args(b),
                        to_args(kv));
   if (int rc = check_hip(hipGetLastError(), "attention_ragged launch")) return rc;
-  RaggedMergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, header, dec, pre, p.max_splits};
+  RaggedMergeArgs m{p.gate, p.ld_gate, p.out, p.num_q_heads, p.num_kv_heads, G, header, dec, pre, p.max_splits,
+                    header + kQueue, claims};
   const size_t mblocks = size_t(b.num_seqs) * p.num_q_heads + s.tasks_bound * (kPrefillRows / kMergeWaves);
   hipLaunchKernelGGL(attn_ragged_merge_kernel, dim3(unsigned(mblocks)), dim3(kMergeThreads), 0, stream, m,
                      to_args(b));

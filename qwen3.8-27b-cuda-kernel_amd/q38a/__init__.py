@@ -85,6 +85,7 @@ _SIGS = {
     "q38a_attention_decode": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_attention_prefill": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_attention_ragged": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
+    "q38a_ragged_scratch_init": (_i, [_p, _p]),
     "q38a_kv_cache_create": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_p)]),
     "q38a_kv_cache_destroy": (None, [_p]),
     "q38a_kv_cache_desc_get": (_i, [_p, _PKv]),
@@ -148,6 +149,11 @@ def attention_decode(params, batch, kv, stream=0):
 
 def attention_prefill(params, batch, kv, stream=0):
     _check(lib.q38a_attention_prefill(ctypes.byref(params), ctypes.byref(batch), ctypes.byref(kv), stream))
+
+
+def ragged_scratch_init(scratch_ptr, stream=0):
+    """Zero the work counters at the front of a ragged scratch buffer (once per new buffer)."""
+    _check(lib.q38a_ragged_scratch_init(scratch_ptr, stream))
 
 
 def attention_ragged(params, batch, kv, stream=0):

@@ -172,7 +172,7 @@ class RaggedBatch:
         self.q16 = torch.empty((self.M, NQ * HD), dtype=torch.float16, device="cuda")
         self.out = torch.empty((self.M, NQ * HD), dtype=torch.bfloat16, device="cuda")
         self.max_splits = 256
-        self.scratch = torch.empty(q38a.ragged_scratch_floats(self.B, self.M, max(n for _, n in self.seqs), NQ, NKV,
+        self.scratch = torch.zeros(q38a.ragged_scratch_floats(self.B, self.M, max(n for _, n in self.seqs), NQ, NKV,
                                                               self.max_splits), dtype=torch.float32, device="cuda")
 
     kv_desc = DecodeBatch.kv_desc

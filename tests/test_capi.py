@@ -82,14 +82,14 @@ def test_rope_table_rejects_other_rotary_dims():
 
 
 def test_ragged_scratch_size_and_refusals():
-    # header (4096 ints) + decode partials [B][nq][splits][258] fp32 + prefill units (tiles bound + 256)
-    # x 256 rows x 132 floats (fp16 O / l [256], m, l, pad)
+    # header (4096 ints) + claim counters (4096 x 32 ints) + decode partials [B][nq][splits][258] fp32
+    # + prefill units (tiles bound + 256) x 256 rows x 132 floats (fp16 O / l [256], m, l, pad)
     B, M, nq, nkv, splits = 8, 519, 24, 4, 64
     tiles = nkv * (M * (nq // nkv) // 256 + B)
-    want = 4096 + B * nq * splits * 258 + (tiles + 256) * 256 * 132
+    want = 4096 + 4096 * 32 + B * nq * splits * 258 + (tiles + 256) * 256 * 132
     assert q38a.ragged_scratch_floats(B, M, 512, nq, nkv, splits) == want
     # all-decode batches need no prefill partials
-    assert q38a.ragged_scratch_floats(B, B, 1, nq, nkv, splits) == 4096 + B * nq * splits * 258
+    assert q38a.ragged_scratch_floats(B, B, 1, nq, nkv, splits) == 4096 + 4096 * 32 + B * nq * splits * 258
     assert q38a.ragged_scratch_floats(0, 1, 1, nq, nkv, splits) == 0
     assert q38a.ragged_scratch_floats(1, 1, 1, 24, 5, splits) == 0
     # refused before any device call

@@ -8,34 +8,52 @@ import torch
 
 import q38a
 from gpu_util import HD, LD, NKV, NQ, Batch, Pool, append_params, attention_params, dev, host, paged_layout, rope_dev, stream
-from util import assert_bits_equal, bf16_bits_to_f32, check_close, randn_bf16
+from util import assert_bits_equal, bf16_bits_to_f32, check_close, f32_to_bf16_bits, randn_bf16
 
 pytestmark = pytest.mark.gpu
 
 
-def build_context(orc, rng, ctxs, kv_dtype, bt, pages, nkv=NKV):
-    """Prior K/V for positions [0, ctx) of every sequence: bf16 N(0,1) rows through the reference
-    quantizer (or bf16 store), written into a host pool."""
+def build_context(orc, rng, ctxs, kv_dtype, bt, pages, nkv=NKV, k_scale=1.0, v_scale=1.0, dominant=None):
+    """Prior K/V for positions [0, ctx) of every sequence: bf16 N(0, scale^2) rows through the
+    reference quantizer (or bf16 store), written into a host pool. dominant = (position, factor):
+    that key row of every sequence is multiplied by factor (one key then dominates the softmax of
+    about half of the heads)."""
     pool = np.zeros(q38a.page_bytes(kv_dtype, nkv) * pages, np.uint8)
     for b, ctx in enumerate(ctxs):
         if ctx == 0:
             continue
-        k = bf16_bits_to_f32(randn_bf16(rng, (ctx, nkv, HD)))
-        v = bf16_bits_to_f32(randn_bf16(rng, (ctx, nkv, HD)))
+        k = bf16_bits_to_f32(randn_bf16(rng, (ctx, nkv, HD), k_scale))
+        v = bf16_bits_to_f32(randn_bf16(rng, (ctx, nkv, HD), v_scale))
+        if dominant is not None and dominant[0] < ctx:
+            k[dominant[0]] = bf16_bits_to_f32(f32_to_bf16_bits(k[dominant[0]] * np.float32(dominant[1])))
         orc.fill_rows(k, v, 0, b, nkv, pool, kv_dtype, bt)
     return pool
 
 
-def decode_step(orc, ctxs, kv_dtype, seed, max_splits=64, check_pool=True, bt_override=None, return_out=False):
+def scale_proj_kv(rng, proj, k_scale, v_scale, nq=NQ, nkv=NKV):
+    """The new tokens' k and v columns of proj redrawn at the given scales (k is RMS-normalised by
+    the append, so only v's scale reaches the cache)."""
+    M = proj.shape[0]
+    k0, v0 = 2 * nq * HD, 2 * nq * HD + nkv * HD
+    proj[:, k0:v0] = randn_bf16(rng, (M, nkv * HD), k_scale)
+    proj[:, v0:v0 + nkv * HD] = randn_bf16(rng, (M, nkv * HD), v_scale)
+    return proj
+
+
+def decode_step(orc, ctxs, kv_dtype, seed, max_splits=64, check_pool=True, bt_override=None, return_out=False,
+                k_scale=1.0, v_scale=1.0, dominant=None):
     rng = np.random.default_rng(seed)
     B = len(ctxs)
     bt, pages = paged_layout(rng, [c + 1 for c in ctxs])
     if bt_override is not None:
         bt = bt_override
-    pool_host = build_context(orc, rng, ctxs, kv_dtype, bt, pages)
+    pool_host = build_context(orc, rng, ctxs, kv_dtype, bt, pages, k_scale=k_scale, v_scale=v_scale,
+                              dominant=dominant)
     pool = Pool(kv_dtype, pages, bt, fill=pool_host)
     b = Batch([(i, c, 1) for i, c in enumerate(ctxs)])
     proj = randn_bf16(rng, (B, LD))
+    if k_scale != 1.0 or v_scale != 1.0:
+        proj = scale_proj_kv(rng, proj, k_scale, v_scale)
     q_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
     k_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
     proj_t, qn_t, kn_t = dev(proj), dev(q_norm), dev(k_norm)

@@ -11,21 +11,25 @@ import torch
 import q38a
 from gpu_util import HD, LD, NKV, NQ, Batch, Pool, append_params, attention_params, dev, host, paged_layout, rope_dev, stream
 from util import assert_bits_equal, bf16_bits_to_f32, check_close, randn_bf16
-from test_gpu_decode import build_context
+from test_gpu_decode import build_context, scale_proj_kv
 
 pytestmark = pytest.mark.gpu
 
 
-def ragged_step(orc, seqs, seed, kv_dtype=q38a.KV_INT8, check_tokens=None, max_splits=64, compare_split_launches=False):
+def ragged_step(orc, seqs, seed, kv_dtype=q38a.KV_INT8, check_tokens=None, max_splits=64, compare_split_launches=False,
+                k_scale=1.0, v_scale=1.0, dominant=None, return_out=False):
     """seqs: [(prefix, n)]; n == 1 is a decode row. check_tokens: per sequence, the chunk-token
     indices compared with the oracle (default all)."""
     rng = np.random.default_rng(seed)
     B = len(seqs)
     bt, pages = paged_layout(rng, [p + n for p, n in seqs])
-    pool_host = build_context(orc, rng, [p for p, _ in seqs], kv_dtype, bt, pages)
+    pool_host = build_context(orc, rng, [p for p, _ in seqs], kv_dtype, bt, pages, k_scale=k_scale, v_scale=v_scale,
+                              dominant=dominant)
     pool = Pool(kv_dtype, pages, bt, fill=pool_host)
     b = Batch([(i, p, n) for i, (p, n) in enumerate(seqs)])
     proj = randn_bf16(rng, (b.M, LD))
+    if k_scale != 1.0 or v_scale != 1.0:
+        proj = scale_proj_kv(rng, proj, k_scale, v_scale)
     q_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
     k_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
     proj_t, qn_t, kn_t = dev(proj), dev(q_norm), dev(k_norm)
@@ -33,6 +37,7 @@ def ragged_step(orc, seqs, seed, kv_dtype=q38a.KV_INT8, check_tokens=None, max_s
     out_t = torch.zeros(b.M * NQ * HD, dtype=torch.int16, device="cuda")
     nfl = q38a.ragged_scratch_floats(B, b.M, max(n for _, n in seqs), NQ, NKV, max_splits)
     scratch_t = torch.full((nfl,), float("nan"), dtype=torch.float32, device="cuda")
+    q38a.ragged_scratch_init(scratch_t.data_ptr(), stream())  # counters zero, partials stay NaN
     rope_t = rope_dev(max(p + n for p, n in seqs) + 1)
     print(f"ragged: seqs={seqs[:10]} dtype={kv_dtype} scratch={nfl * 4 / 2**20:.1f} MiB", flush=True)
     q38a.qk_norm_rope_append(append_params(proj_t, qn_t, kn_t, q_t, rope_t), b.desc, pool.desc, stream())
@@ -65,6 +70,8 @@ def ragged_step(orc, seqs, seed, kv_dtype=q38a.KV_INT8, check_tokens=None, max_s
                                 kv_dtype, bt)
     want = bf16_bits_to_f32(want).reshape(len(sel), NQ * HD)
     assert np.isfinite(got[sel]).all()
+    if return_out:
+        return got[sel], want
     return check_close(got[sel], want, what=f"ragged seqs={seqs[:10]}")
 
 
