@@ -139,6 +139,17 @@ size_t q38a_split_scratch_floats(int rows, int num_q_heads, int max_splits);
 int q38a_attention_decode(const q38a_attention_params* p, const q38a_batch_desc* batch,
                           const q38a_kv_cache_desc* kv, void* stream);
 
+/* q38a_attention_decode without caller scratch: the split partials go to a static device array
+ * of q38a_noalloc_scratch_floats() floats (32 MiB, one per GPU, held until the process ends) and
+ * p->split_scratch is ignored; the call allocates nothing (no hipMalloc, no library allocation).
+ * Fails with Q38A_ERR_INVALID when num_seqs * num_q_heads * max_splits * 258 exceeds the array.
+ * Every call on one GPU shares the array: calls that overlap in time on one GPU race.
+ * No counterpart in the reference; for callers that cannot allocate (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid allocation). */
+int q38a_attention_decode_noalloc(const q38a_attention_params* p, const q38a_batch_desc* batch,
+                                  const q38a_kv_cache_desc* kv, void* stream);
+size_t q38a_noalloc_scratch_floats(void);
+
 /* Prefill: causal attention of each sequence's new tokens over its cached prefix and themselves
  * (the chunk's K/V must already be appended); fp16 MFMA, gate in the epilogue. Replaces
  * reference kernels.h:178-179 attention_prefill (src/kernels/attention_prefill.cu:317-335). */

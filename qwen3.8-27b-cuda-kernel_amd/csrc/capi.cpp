@@ -20,6 +20,9 @@ int launch_attention_prefill(const q38a_attention_params& p, const q38a_batch_de
 int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
                             hipStream_t stream);
 int ragged_scratch_init(float* scratch, hipStream_t stream);
+int launch_attention_decode_noalloc(const q38a_attention_params& p, const q38a_batch_desc& b,
+                                    const q38a_kv_cache_desc& kv, hipStream_t stream);
+size_t noalloc_scratch_floats();
 int max_group();
 size_t ragged_scratch_floats(int num_seqs, int num_tokens, int max_tokens_per_seq, int nq, int nkv, int max_splits);
 
@@ -216,6 +219,19 @@ int q38a_attention_decode(const q38a_attention_params* p, const q38a_batch_desc*
                      batch->num_tokens, batch->num_seqs);
   return launch_attention_decode(*p, *batch, *kv, static_cast<hipStream_t>(stream));
 }
+
+int q38a_attention_decode_noalloc(const q38a_attention_params* p, const q38a_batch_desc* batch,
+                                  const q38a_kv_cache_desc* kv, void* stream) {
+  clear_error();
+  if (int rc = validate_attention(p, batch, kv, false)) return rc;
+  if (p->max_splits <= 0) return set_error(Q38A_ERR_INVALID, "attention_decode_noalloc: max_splits must be positive");
+  if (batch->num_tokens != batch->num_seqs)
+    return set_error(Q38A_ERR_INVALID, "attention_decode_noalloc: one token per sequence required (M %d, B %d)",
+                     batch->num_tokens, batch->num_seqs);
+  return launch_attention_decode_noalloc(*p, *batch, *kv, static_cast<hipStream_t>(stream));
+}
+
+size_t q38a_noalloc_scratch_floats(void) { return noalloc_scratch_floats(); }
 
 int q38a_attention_prefill(const q38a_attention_params* p, const q38a_batch_desc* batch,
                            const q38a_kv_cache_desc* kv, void* stream) {

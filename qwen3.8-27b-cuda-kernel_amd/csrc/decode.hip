@@ -1,5 +1,8 @@
 // Split-KV decode launch (q38a_attention_decode) and its gated split merge; the device code is in
 // decode.hpp.
+#include <mutex>
+#include <vector>
+
 #include "decode.hpp"
 
 namespace q38a {
@@ -79,6 +82,53 @@ int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_des
   hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(kMergeThreads), 0, stream, m,
                      to_args(b));
   return check_hip(hipGetLastError(), "attention merge launch");
+}
+
+// ---- decode without caller scratch --------------------------------------------------------------
+// For callers that cannot allocate (code under graph capture, tight serving loops): the split
+// partials go to a file-scope device array instead of p.split_scratch. Each GPU holds its own copy
+// for the life of the process; every call on a GPU shares it, so calls that overlap in time on one
+// GPU race (the decode partials need no clearing: the merge reads only splits the decode kernel of
+// the same call wrote).
+constexpr size_t kNoAllocScratchFloats = size_t(8) << 20;  // 32 MiB per GPU
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device (the array's name
+// is a host-side stand-in: only this address may be passed to kernels).
+int noalloc_scratch(float** out) {
+  static std::mutex mu;
+  static std::vector<float*> ptrs;
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "attention_decode_noalloc: hipGetDevice")) return rc;
+  std::lock_guard<std::mutex> lock(mu);
+  if (int(ptrs.size()) <= dev) ptrs.resize(size_t(dev) + 1, nullptr);
+  if (!ptrs[size_t(dev)]) {
+    void* p = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "attention_decode_noalloc: hipGetSymbolAddress"))
+      return rc;
+    ptrs[size_t(dev)] = static_cast<float*>(p);
+  }
+  *out = ptrs[size_t(dev)];
+  return Q38A_OK;
+}
+
+}  // namespace
+
+size_t noalloc_scratch_floats() { return kNoAllocScratchFloats; }
+
+int launch_attention_decode_noalloc(const q38a_attention_params& p, const q38a_batch_desc& b,
+                                    const q38a_kv_cache_desc& kv, hipStream_t stream) {
+  const size_t need = size_t(b.num_seqs) * size_t(p.num_q_heads) * size_t(p.max_splits) * (kHeadDim + 2);
+  if (need > kNoAllocScratchFloats)
+    return set_error(Q38A_ERR_INVALID,
+                     "attention_decode_noalloc: %d rows x %d q heads x %d splits need %zu scratch floats; the "
+                     "static scratch holds %zu",
+                     b.num_seqs, p.num_q_heads, p.max_splits, need, kNoAllocScratchFloats);
+  q38a_attention_params q = p;
+  if (int rc = noalloc_scratch(&q.split_scratch)) return rc;
+  return launch_attention_decode(q, b, kv, stream);
 }
 
 }  // namespace q38a

@@ -86,6 +86,8 @@ _SIGS = {
     "q38a_attention_prefill": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_attention_ragged": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_ragged_scratch_init": (_i, [_p, _p]),
+    "q38a_attention_decode_noalloc": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
+    "q38a_noalloc_scratch_floats": (_sz, []),
     "q38a_kv_cache_create": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_p)]),
     "q38a_kv_cache_destroy": (None, [_p]),
     "q38a_kv_cache_desc_get": (_i, [_p, _PKv]),
@@ -149,6 +151,15 @@ def attention_decode(params, batch, kv, stream=0):
 
 def attention_prefill(params, batch, kv, stream=0):
     _check(lib.q38a_attention_prefill(ctypes.byref(params), ctypes.byref(batch), ctypes.byref(kv), stream))
+
+
+def attention_decode_noalloc(params, batch, kv, stream=0):
+    """q38a_attention_decode with the split partials in the library's static device array."""
+    _check(lib.q38a_attention_decode_noalloc(ctypes.byref(params), ctypes.byref(batch), ctypes.byref(kv), stream))
+
+
+def noalloc_scratch_floats():
+    return lib.q38a_noalloc_scratch_floats()
 
 
 def ragged_scratch_init(scratch_ptr, stream=0):
