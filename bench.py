@@ -61,6 +61,36 @@ def time_attention_only(batch, steps, rotate):
     return sum(a.elapsed_time(b) for a, b in evs) / steps
 
 
+def measured_peaks(reps=10):
+    """The ceilings this GPU reaches (include/q38a_probe.h): HBM read rate of a 4 GiB buffer with
+    16-byte loads, and the fp16 MFMA issue rate of register-only MFMA chains. HIP events on the
+    launch stream; the best of `reps` launches."""
+    import torch
+    from q38a import probe
+    s = torch.cuda.current_stream().cuda_stream
+    nbytes = 4 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    sink = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    best_read = best_mfma = 0.0
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        probe.read(buf.data_ptr(), nbytes, sink.data_ptr(), 1024, s)
+        b.record()
+        torch.cuda.synchronize()
+        best_read = max(best_read, nbytes / (a.elapsed_time(b) * 1e-3) / 1e9)
+    del buf
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fl = probe.mfma(sink.data_ptr(), 2000, s)
+        b.record()
+        torch.cuda.synchronize()
+        best_mfma = max(best_mfma, fl / (a.elapsed_time(b) * 1e-3) / 1e12)
+    return {"hbm_read_gbs": round(best_read, 1), "mfma_fp16_tflops": round(best_mfma, 1)}
+
+
 def decode_config(name, dtype, steps, warmup, pools=3):
     import torch
     import q38a
@@ -244,6 +274,13 @@ def profile_workload(name, reps=20):
         torch.neg(x, out=y)
     torch.cuda.synchronize()
     print("profile copy: 4 x (1 GiB read + 1 GiB written)", flush=True)
+    del x, y
+    from q38a import probe
+    sink = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    for _ in range(2):
+        probe.mfma(sink.data_ptr(), 2000, s)
+    torch.cuda.synchronize()
+    print("profile mfma probe: 2 launches (MFMA-busy calibration)", flush=True)
 
 
 def _csv_rows(d, suffix):
@@ -293,6 +330,45 @@ def pmc_summary(fetch_dir, write_dir, out=None):
         open(out, "w").write(text + "\n")
 
 
+def mfma_summary(d, out=None, simds=1024):
+    """MFMA utilisation per kernel from a rocprofv3 --pmc run of SQ_VALU_MFMA_BUSY_CYCLES,
+    GRBM_GUI_ACTIVE and SQ_INSTS_VALU_MFMA_MOPS_F16 over `bench.py --profile`: busy fraction =
+    sum of MFMA-busy cycles over all SIMDs / (GPU-active cycles x SIMDs) (rocprofv3's own MFMA_UTIL
+    expression), and the fp16 flops the MFMAs did (MOPS x 512). The MFMA probe kernel, which does
+    nothing but MFMAs, gives the fraction that counts as fully busy."""
+    import collections
+    per = collections.defaultdict(lambda: collections.defaultdict(lambda: collections.defaultdict(float)))
+    for r in _csv_rows(d, "counter_collection.csv"):
+        k = r["Kernel_Name"]
+        disp = r.get("Dispatch_Id") or r.get("Correlation_Id") or "0"
+        name = r["Counter_Name"]
+        v = float(r["Counter_Value"])
+        if name == "GRBM_GUI_ACTIVE":
+            per[k][disp][name] = max(per[k][disp][name], v)
+        else:
+            per[k][disp][name] += v
+    rows = []
+    for k, disps in per.items():
+        util = [x["SQ_VALU_MFMA_BUSY_CYCLES"] / (x["GRBM_GUI_ACTIVE"] * simds) for x in disps.values()
+                if x["GRBM_GUI_ACTIVE"] > 0]
+        fl = [x["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512 for x in disps.values()]
+        if util:
+            rows.append((short_name(k), len(util), sum(util) / len(util), sum(fl) / len(fl)))
+    probe = [r for r in rows if "mfma_probe" in r[0]]
+    ref = probe[0][2] if probe else None
+    lines = [f"mfma probe busy fraction (calibration, counts as 1.0): {ref:.4f}" if ref else "no probe",
+             "| kernel | dispatches | MFMA busy (raw) | MFMA busy / probe | fp16 MFMA flops per dispatch |",
+             "|---|---|---|---|---|"]
+    for name, n, u, f in sorted(rows):
+        if not name.startswith("q38a::"):
+            continue
+        lines.append(f"| {name} | {n} | {u:.4f} | {u / ref if ref else float('nan'):.4f} | {f:.4g} |")
+    text = "\n".join(lines)
+    print(text)
+    if out:
+        open(out, "w").write(text + "\n")
+
+
 def short_name(n):
     n = n.replace("(anonymous namespace)::", "").replace("void ", "")
     return n.split("(")[0][:80]
@@ -317,6 +393,21 @@ def read_traffic(workload):
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":")[1])
     return None
+
+
+def read_mfma_busy():
+    """MFMA busy fraction (relative to the probe) of the attention kernel of the prefill and mixed
+    workloads, from profiles/attention_<workload>_mfma.txt, or {}."""
+    out = {}
+    for w, kern in (("prefill", "attn_prefill"), ("mixed", "attn_ragged_kernel")):
+        path = os.path.join(ROOT, "profiles", f"attention_{w}_mfma.txt")
+        if not os.path.exists(path):
+            continue
+        for line in open(path):
+            cells = [c.strip() for c in line.split("|")]
+            if len(cells) > 4 and kern in cells[1]:
+                out[w] = float(cells[4])
+    return out
 
 
 def cpu_baseline(batch, budget_s=20.0):
@@ -415,7 +506,10 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--pmc-out", default=None)
     ap.add_argument("--stats-summary", metavar="DIR")
+    ap.add_argument("--mfma-summary", metavar="DIR")
     args = ap.parse_args()
+    if args.mfma_summary:
+        return mfma_summary(args.mfma_summary, out=args.pmc_out)
     if args.pmc_summary:
         return pmc_summary(*args.pmc_summary, out=args.pmc_out)
     if args.stats_summary:
@@ -451,6 +545,17 @@ def main():
     if not only or "prefill_ragged" in only:
         extra["prefill_2048_on_6000_ragged"] = ragged_config("prefill_2048_on_6000_ragged", [(6000, 2048)],
                                                              max(10, args.steps // 5), 3, pools=1)
+    peaks = measured_peaks()
+    for r in extra.values():
+        if "attn_gbs" in r:
+            r["hbm_frac_of_measured"] = round(r["attn_gbs"] / peaks["hbm_read_gbs"], 4)
+        if "attn_tflops" in r:
+            r["mfma_frac_of_measured"] = round(r["attn_tflops"] / peaks["mfma_fp16_tflops"], 4)
+    busy = read_mfma_busy()
+    if busy and "prefill_2048_on_6000" in extra:
+        extra["prefill_2048_on_6000"]["mfma_busy_frac"] = busy.get("prefill")
+    if busy and "mixed_512_plus_7" in extra:
+        extra["mixed_512_plus_7"]["mfma_busy_frac"] = busy.get("mixed")
     batch = head.pop("_batch")
     cpu = None if args.no_cpu else cpu_baseline(batch)
     line = {
@@ -473,7 +578,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_b8"),
                      "kernel": "attention_decode (attn_decode_kernel + attn_merge_kernel)",
-                     "kernel_ms": round(head["attn_ms"], 5)},
+                     "kernel_ms": round(head["attn_ms"], 5),
+                     "measured_peak": peaks["hbm_read_gbs"],
+                     "frac_of_measured": round(head["attn_gbs"] / peaks["hbm_read_gbs"], 4)},
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "tokens_per_s": round(head["tokens_per_s"], 1),
         "extra": extra,

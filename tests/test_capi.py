@@ -32,6 +32,11 @@ def test_every_declared_symbol_is_exported():
     missing = [n for n in rt if not hasattr(lib, n)]
     assert not missing, missing
     assert set(runtime.EXPORTED) == set(rt)
+    from q38a import probe
+    pr = declared_functions("q38a_probe.h")
+    missing = [n for n in pr if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(probe.EXPORTED) == set(pr)
 
 
 def test_page_layout_matches_reference_format():
