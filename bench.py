@@ -91,11 +91,11 @@ def measured_peaks(reps=10):
     return {"hbm_read_gbs": round(best_read, 1), "mfma_fp16_tflops": round(best_mfma, 1)}
 
 
-def decode_config(name, dtype, steps, warmup, pools=3):
+def decode_config(name, dtype, steps, warmup, pools=3, ctx_name=None):
     import torch
     import q38a
     from q38a.workloads import DecodeBatch, decode_contexts
-    ctxs = decode_contexts(name)
+    ctxs = decode_contexts(ctx_name or name)
     batch = DecodeBatch(ctxs, dtype=dtype, seed=0, pools=pools)
     s = torch.cuda.current_stream().cuda_stream
     appp, ap = batch.append_params(), batch.attention_params()
@@ -109,7 +109,7 @@ def decode_config(name, dtype, steps, warmup, pools=3):
     attn_ms = time_attention_only(batch, steps, pools)
     kv = batch.kv_bytes()
     return {
-        "config": name, "ctxs": ctxs, "kv_dtype": "int8" if dtype == q38a.KV_INT8 else "bf16",
+        "config": name, "ctxs": ctxs, "kv_dtype": {0: "int8", 1: "bf16", 2: "int8_vt"}[dtype],
         "ms_per_step": ms, "tokens_per_s": batch.B / (ms * 1e-3),
         "kv_bytes": kv, "kv_gbs": kv / (ms * 1e-3) / 1e9,
         "attn_ms": attn_ms, "attn_gbs": (kv + batch.io_bytes()) / (attn_ms * 1e-3) / 1e9,
@@ -117,12 +117,12 @@ def decode_config(name, dtype, steps, warmup, pools=3):
     }
 
 
-def prefill_config(steps, warmup):
+def prefill_config(steps, warmup, dtype=0):
     """Config 3: one sequence appends a 2048-token chunk onto a 6000-token int8 prefix."""
     import torch
     import q38a
     from q38a.workloads import RaggedBatch
-    rb = RaggedBatch([(6000, 2048)], seed=0)
+    rb = RaggedBatch([(6000, 2048)], dtype=dtype, seed=0)
     s = torch.cuda.current_stream().cuda_stream
     appp, ap, kvd = rb.append_params(), rb.attention_params(), rb.kv_desc(0)
 
@@ -144,14 +144,14 @@ def prefill_config(steps, warmup):
             "mfma_frac": round(fl / (attn_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
 
 
-def ragged_config(name, seqs, steps, warmup, pools=3):
+def ragged_config(name, seqs, steps, warmup, pools=3, dtype=0):
     """One continuous-batching step through the single ragged launch (q38a_attention_ragged):
     append of every new token, then decode rows and prefill chunks together. Config 4 is one
     512-token chunk + 7 decode rows; t_roof = decode KV bytes / HBM peak + prefill flops / MFMA peak."""
     import torch
     import q38a
     from q38a.workloads import RaggedBatch
-    rb = RaggedBatch(seqs, seed=0, pools=pools)
+    rb = RaggedBatch(seqs, dtype=dtype, seed=0, pools=pools)
     s = torch.cuda.current_stream().cuda_stream
     appp, ap = rb.append_params(), rb.attention_params()
     descs = [rb.kv_desc(i) for i in range(pools)]
@@ -243,19 +243,21 @@ def profile_workload(name, reps=20):
     import q38a
     from q38a.workloads import DecodeBatch, RaggedBatch, decode_contexts, mixed_seqs
     s = torch.cuda.current_stream().cuda_stream
-    if name in ("decode_b8", "long_b8", "long_b1", "long_b8_bf16"):
-        dt = q38a.KV_BF16 if name.endswith("bf16") else q38a.KV_INT8
-        b = DecodeBatch(decode_contexts(name), dtype=dt, seed=0, pools=3)
+    vt = name.endswith("_int8_vt")  # the same workload on int8 VT pages
+    base = name[:-len("_int8_vt")] if vt else name
+    if base in ("decode_b8", "long_b8", "long_b1", "long_b8_bf16"):
+        dt = q38a.KV_INT8_VT if vt else (q38a.KV_BF16 if base.endswith("bf16") else q38a.KV_INT8)
+        b = DecodeBatch(decode_contexts(base), dtype=dt, seed=0, pools=3)
         ap, descs = b.attention_params(), [b.kv_desc(i) for i in range(3)]
         q38a.qk_norm_rope_append(b.append_params(), b.batch, descs[0], s)
         run = lambda i: q38a.attention_decode(ap, b.batch, descs[i % 3], s)  # noqa: E731
-    elif name == "prefill":
-        rb = RaggedBatch([(6000, 2048)], seed=0)
+    elif base == "prefill":
+        rb = RaggedBatch([(6000, 2048)], dtype=q38a.KV_INT8_VT if vt else q38a.KV_INT8, seed=0)
         ap, kvd = rb.attention_params(), rb.kv_desc(0)
         q38a.qk_norm_rope_append(rb.append_params(), rb.batch, kvd, s)
         run = lambda i: q38a.attention_prefill(ap, rb.batch, kvd, s)  # noqa: E731
-    elif name == "mixed":
-        rb = RaggedBatch(mixed_seqs(0), seed=0, pools=3)
+    elif base == "mixed":
+        rb = RaggedBatch(mixed_seqs(0), dtype=q38a.KV_INT8_VT if vt else q38a.KV_INT8, seed=0, pools=3)
         ap, descs = rb.attention_params(), [rb.kv_desc(i) for i in range(3)]
         q38a.qk_norm_rope_append(rb.append_params(), rb.batch, descs[0], s)
         run = lambda i: q38a.attention_ragged(ap, rb.batch, descs[i % 3], s)  # noqa: E731
@@ -315,7 +317,7 @@ def pmc_summary(fetch_dir, write_dir, out=None):
              "|---|---|---|---|---|---|"]
     total = 0.0  # the attention launch: q38a attention and merge kernels
     for n in names:
-        if n in copy:
+        if n in copy or not short_name(n).startswith("q38a::"):
             continue
         f, w = vals.get((n, "FETCH_SIZE"), [0.0]), vals.get((n, "WRITE_SIZE"), [0.0])
         fm, wm = sum(f) / len(f), sum(w) / len(w)
@@ -450,7 +452,7 @@ def cpu_baseline(batch, budget_s=20.0):
             dt = time.perf_counter() - t0
         spent += dt
         done_tokens += 1
-        done_bytes += L * (2112 if batch.dtype == q38a.KV_INT8 else 4096)
+        done_bytes += L * (4096 if batch.dtype == q38a.KV_BF16 else 2112)
         if spent > budget_s:
             break
     out = {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
@@ -527,19 +529,27 @@ def main():
     only = set(filter(None, args.only.split(",")))
     extra = {}
     head = decode_config("decode_b8", q38a.KV_INT8, args.steps, args.warmup)
-    for name, dt in (("long_b8", q38a.KV_INT8), ("long_b1", q38a.KV_INT8), ("long_b8_bf16", q38a.KV_BF16)):
+    for name, dt, cn in (("long_b8", q38a.KV_INT8, None), ("long_b1", q38a.KV_INT8, None),
+                         ("long_b8_bf16", q38a.KV_BF16, None), ("decode_b8_int8_vt", q38a.KV_INT8_VT, "decode_b8"),
+                         ("long_b8_int8_vt", q38a.KV_INT8_VT, "long_b8")):
         if only and name not in only:
             continue
-        r = decode_config(name, dt, args.steps, args.warmup)
+        r = decode_config(name, dt, args.steps, args.warmup, ctx_name=cn)
         r.pop("_batch")
         r["hbm_frac"] = r["attn_gbs"] / HBM_PEAK_GBS
         extra[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items() if k != "ctxs"}
         extra[name]["sum_ctx"] = sum(r["ctxs"])
     if not only or "prefill" in only:
         extra["prefill_2048_on_6000"] = prefill_config(max(10, args.steps // 5), 3)
+    if not only or "prefill_int8_vt" in only:
+        extra["prefill_2048_on_6000_int8_vt"] = prefill_config(max(10, args.steps // 5), 3, dtype=q38a.KV_INT8_VT)
     if not only or "mixed" in only:
         from q38a.workloads import mixed_seqs
         extra["mixed_512_plus_7"] = ragged_config("mixed_512_plus_7", mixed_seqs(0), max(10, args.steps // 2), 3)
+    if not only or "mixed_int8_vt" in only:
+        from q38a.workloads import mixed_seqs
+        extra["mixed_512_plus_7_int8_vt"] = ragged_config("mixed_512_plus_7_int8_vt", mixed_seqs(0),
+                                                          max(10, args.steps // 2), 3, dtype=q38a.KV_INT8_VT)
     if not only or "runner" in only:
         extra["decode_b8_16_layers_runner"] = runner_decode_config(max(10, args.steps // 5), 3)
     if not only or "prefill_ragged" in only:

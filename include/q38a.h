@@ -30,8 +30,13 @@ extern "C" {
 #define Q38A_PAGE_TOKENS 64 /* reference kernels.h:38 kPageTokens */
 #define Q38A_HEAD_DIM 256   /* reference kernels.h:39 kHeadDim */
 
-/* KV page formats (reference kernels.h:36 KvDtype). */
-enum { Q38A_KV_INT8 = 0, Q38A_KV_BF16 = 1 };
+/* KV page formats. INT8 and BF16 are the reference's (kernels.h:36 KvDtype). INT8_VT is the
+ * "tensor-core decode" variant of the int8 format (reference docs/OPTIMIZATION_PLAN.md:199-201):
+ * the same bytes per page, K codes and K scales laid out as in INT8, but the V codes stored
+ * transposed within each 16-token quarter of the page, [kvh][4 quarters][256 dims][16 tokens]
+ * (a dim's 16 tokens contiguous, consecutive dims adjacent), and the V scales group-major,
+ * [kvh][4 groups][64 tokens] f16. */
+enum { Q38A_KV_INT8 = 0, Q38A_KV_BF16 = 1, Q38A_KV_INT8_VT = 2 };
 
 /* Status codes. */
 enum {
@@ -78,7 +83,9 @@ typedef struct q38a_kv_cache_desc {
 size_t q38a_kv_page_bytes(int dtype, int kv_heads);
 
 /* Byte offsets inside one (layer, page) block (reference kernels.h:53-65):
- * out[0] K row, out[1] V row, out[2] K scales, out[3] V scales (scales: int8 only). */
+ * out[0] K row, out[1] V row, out[2] K scales, out[3] V scales (scales: int8 formats only).
+ * INT8_VT: out[1] is the V code of (head, dim 0, tok) (dim d at + 16 d) and out[3] the V scale of
+ * (head, group 0, tok) (group g at + 128 g). */
 int q38a_kv_offsets(int dtype, int kv_heads, int head, int tok, size_t out[4]);
 
 /* ---- fused q/k RMSNorm + RoPE + KV append ------------------------------------------------- */

@@ -107,19 +107,31 @@ void rope_apply(float* y, int rotary_dim, const float* cs) {
 }
 
 // ---- paged layout (kernels.h:41-70) -----------------------------------------------------------
+// dtype 0: int8 (reference), 1: bf16 (reference), 2: int8 with V transposed per page (this
+// library's variant of the int8 format: the same codes and scales at other offsets, V^T
+// [kvh][4 quarters][256][16 tokens], V scales [kvh][4][64]; K and its scales as in dtype 0).
 struct Layout {
   int kv_heads;
-  int dtype;  // 0 int8, 1 bf16
-  size_t elem() const { return dtype == 0 ? 1 : 2; }
+  int dtype;
+  bool int8() const { return dtype != 1; }
+  size_t elem() const { return int8() ? 1 : 2; }
   size_t k_off(int h, int t) const { return (size_t(h) * kPageTokens + t) * kHeadDim * elem(); }
   size_t v_off(int h, int t) const { return size_t(kv_heads) * kPageTokens * kHeadDim * elem() + k_off(h, t); }
   size_t ks_off(int h, int t) const {
     return 2 * size_t(kv_heads) * kPageTokens * kHeadDim + (size_t(h) * kPageTokens + t) * 8;
   }
   size_t vs_off(int h, int t) const { return ks_off(h, t) + size_t(kv_heads) * kPageTokens * 8; }
+  // dtype 2: V code of (h, dim d, token t) and V scale of (h, group g, token t)
+  size_t vt_code_off(int h, int d, int t) const {
+    return size_t(kv_heads) * kPageTokens * kHeadDim + ((size_t(h) * 4 + t / 16) * kHeadDim + d) * 16 + t % 16;
+  }
+  size_t vt_scale_off(int h, int g, int t) const {
+    return 2 * size_t(kv_heads) * kPageTokens * kHeadDim + size_t(kv_heads) * kPageTokens * 8 +
+           ((size_t(h) * 4 + g) * kPageTokens + t) * 2;
+  }
   size_t page_bytes() const {
-    return dtype == 0 ? 2 * size_t(kv_heads) * kPageTokens * (kHeadDim + 8)
-                      : 2 * size_t(kv_heads) * kPageTokens * kHeadDim * 2;
+    return int8() ? 2 * size_t(kv_heads) * kPageTokens * (kHeadDim + 8)
+                  : 2 * size_t(kv_heads) * kPageTokens * kHeadDim * 2;
   }
 };
 
@@ -127,6 +139,15 @@ void store_row(uint8_t* page, const Layout& L, bool is_v, int h, int t, const fl
   if (L.dtype == 1) {
     uint16_t* dst = reinterpret_cast<uint16_t*>(page + (is_v ? L.v_off(h, t) : L.k_off(h, t)));
     for (int d = 0; d < kHeadDim; ++d) dst[d] = f32_to_bf16(y[d]);
+    return;
+  }
+  if (L.dtype == 2 && is_v) {  // same quantisation, codes scattered down the V^T columns
+    int8_t codes[kHeadDim];
+    for (int g = 0; g < 4; ++g) {
+      const uint16_t s = quantize_group(y + 64 * g, codes + 64 * g);
+      std::memcpy(page + L.vt_scale_off(h, g, t), &s, 2);
+    }
+    for (int d = 0; d < kHeadDim; ++d) page[L.vt_code_off(h, d, t)] = uint8_t(codes[d]);
     return;
   }
   int8_t* dst = reinterpret_cast<int8_t*>(page + (is_v ? L.v_off(h, t) : L.k_off(h, t)));
@@ -138,6 +159,14 @@ void load_row(const uint8_t* page, const Layout& L, bool is_v, int h, int t, flo
   if (L.dtype == 1) {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(page + (is_v ? L.v_off(h, t) : L.k_off(h, t)));
     for (int d = 0; d < kHeadDim; ++d) out[d] = bf16_to_f32(src[d]);
+    return;
+  }
+  if (L.dtype == 2 && is_v) {
+    for (int d = 0; d < kHeadDim; ++d) {
+      uint16_t s;
+      std::memcpy(&s, page + L.vt_scale_off(h, d / 64, t), 2);
+      out[d] = float(int8_t(page[L.vt_code_off(h, d, t)])) * f16_to_f32(s);
+    }
     return;
   }
   const int8_t* src = reinterpret_cast<const int8_t*>(page + (is_v ? L.v_off(h, t) : L.k_off(h, t)));

@@ -180,6 +180,7 @@ __device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, double*
   if (!store_ok) return;
   const int tok = pos % kPageTokens;
   uint8_t* base = kv.pool + size_t(p.attn_layer) * kv.layer_stride + size_t(page) * kv.page_bytes;
+  const bool vt = !is_k && kv.layout.dtype == Q38A_KV_INT8_VT;  // V codes transposed, scales group-major
   const size_t row = is_k ? kv.layout.k_row(head, tok) : kv.layout.v_row(head, tok);
 
   if (kv.layout.dtype == Q38A_KV_BF16) {
@@ -202,6 +203,13 @@ __device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, double*
     float q = 0.0f;
     if (scale > 0.0f) q = fminf(fmaxf(__builtin_rintf(div_rn(x[e], scale)), -127.0f), 127.0f);
     packed |= (uint32_t(int32_t(q)) & 0xffu) << (8 * e);
+  }
+  if (vt) {
+    // dim 4 lane + e of this token: byte `tok` of V^T row (head, dim)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) base[kv.layout.vt_code(head, 4 * lane + e, tok)] = uint8_t(packed >> (8 * e));
+    if ((lane & 15) == 0) *reinterpret_cast<uint16_t*>(base + kv.layout.vt_scale(head, lane >> 4, tok)) = sbits;
+    return;
   }
   *reinterpret_cast<uint32_t*>(base + row + 4 * lane) = packed;
   if ((lane & 15) == 0) {

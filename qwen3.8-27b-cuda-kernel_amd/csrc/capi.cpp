@@ -79,7 +79,7 @@ int validate_batch(const q38a_batch_desc* b, bool need_tok) {
 int validate_kv(const q38a_kv_cache_desc* k) {
   if (!k) return set_error(Q38A_ERR_INVALID, "KV descriptor is null");
   if (!k->pool || !k->block_table) return set_error(Q38A_ERR_INVALID, "KV: pool and block_table must be set");
-  if (k->dtype != Q38A_KV_INT8 && k->dtype != Q38A_KV_BF16)
+  if (k->dtype != Q38A_KV_INT8 && k->dtype != Q38A_KV_BF16 && k->dtype != Q38A_KV_INT8_VT)
     return set_error(Q38A_ERR_INVALID, "KV: unknown dtype %d", k->dtype);
   if (k->kv_heads <= 0 || k->num_pages <= 0 || k->max_pages_per_seq <= 0)
     return set_error(Q38A_ERR_INVALID, "KV: kv_heads, num_pages and max_pages_per_seq must be positive");
@@ -128,20 +128,20 @@ extern "C" {
 const char* q38a_last_error(void) { return g_error.c_str(); }
 
 size_t q38a_kv_page_bytes(int dtype, int kv_heads) {
-  if (kv_heads <= 0 || (dtype != Q38A_KV_INT8 && dtype != Q38A_KV_BF16)) return 0;
+  if (kv_heads <= 0 || (dtype != Q38A_KV_INT8 && dtype != Q38A_KV_BF16 && dtype != Q38A_KV_INT8_VT)) return 0;
   return PageLayout{kv_heads, dtype}.page_bytes();
 }
 
 int q38a_kv_offsets(int dtype, int kv_heads, int head, int tok, size_t out[4]) {
   clear_error();
   if (!out || kv_heads <= 0 || head < 0 || head >= kv_heads || tok < 0 || tok >= kPageTokens ||
-      (dtype != Q38A_KV_INT8 && dtype != Q38A_KV_BF16))
+      (dtype != Q38A_KV_INT8 && dtype != Q38A_KV_BF16 && dtype != Q38A_KV_INT8_VT))
     return set_error(Q38A_ERR_INVALID, "kv_offsets: bad arguments");
   const PageLayout L{kv_heads, dtype};
   out[0] = L.k_row(head, tok);
-  out[1] = L.v_row(head, tok);
-  out[2] = dtype == Q38A_KV_INT8 ? L.k_scales(head, tok) : 0;
-  out[3] = dtype == Q38A_KV_INT8 ? L.v_scales(head, tok) : 0;
+  out[1] = dtype == Q38A_KV_INT8_VT ? L.vt_code(head, 0, tok) : L.v_row(head, tok);
+  out[2] = L.int8() ? L.k_scales(head, tok) : 0;
+  out[3] = dtype == Q38A_KV_INT8_VT ? L.vt_scale(head, 0, tok) : (L.int8() ? L.v_scales(head, tok) : 0);
   return Q38A_OK;
 }
 

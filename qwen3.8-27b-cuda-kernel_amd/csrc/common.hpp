@@ -26,10 +26,13 @@ int device_cu_count(int* out);                   // cached per device
 // One (layer, page) block, int8:  K [kvh][64][256] i8 | V [kvh][64][256] i8 |
 //                                 K scales [kvh][64][4] f16 | V scales [kvh][64][4] f16
 //                         bf16:   K [kvh][64][256] bf16 | V [kvh][64][256] bf16
+//                      int8 VT:   K [kvh][64][256] i8 | V^T [kvh][4][256][16] i8 (per 16-token quarter) |
+//                                 K scales [kvh][64][4] f16 | V scales [kvh][4][64] f16
 struct PageLayout {
   int kv_heads;
   int dtype;
-  __host__ __device__ size_t elem() const { return dtype == Q38A_KV_INT8 ? 1 : 2; }
+  __host__ __device__ bool int8() const { return dtype != Q38A_KV_BF16; }  // int8 codes + fp16 scales
+  __host__ __device__ size_t elem() const { return int8() ? 1 : 2; }
   __host__ __device__ size_t k_row(int h, int t) const {
     return (size_t(h) * kPageTokens + t) * kHeadDim * elem();
   }
@@ -43,8 +46,18 @@ struct PageLayout {
     return k_scales(h, t) + size_t(kv_heads) * kPageTokens * 8;
   }
   __host__ __device__ size_t page_bytes() const {
-    return dtype == Q38A_KV_INT8 ? 2 * size_t(kv_heads) * kPageTokens * (kHeadDim + 8)
-                                 : 2 * size_t(kv_heads) * kPageTokens * kHeadDim * 2;
+    return int8() ? 2 * size_t(kv_heads) * kPageTokens * (kHeadDim + 8)
+                  : 2 * size_t(kv_heads) * kPageTokens * kHeadDim * 2;
+  }
+  // int8 VT: V code of (head h, dim d, token t), and V scale of (head h, group g, token t). The
+  // codes of a 16-token quarter are [dim][16 tokens], so token t + 16 is 4,096 bytes further, the
+  // same stride as 16 K rows.
+  __host__ __device__ size_t vt_code(int h, int d, int t) const {
+    return size_t(kv_heads) * kPageTokens * kHeadDim + ((size_t(h) * 4 + t / 16) * kHeadDim + d) * 16 + t % 16;
+  }
+  __host__ __device__ size_t vt_scale(int h, int g, int t) const {
+    return 2 * size_t(kv_heads) * kPageTokens * kHeadDim + size_t(kv_heads) * kPageTokens * 8 +
+           ((size_t(h) * 4 + g) * kPageTokens + t) * 2;
   }
 };
 

@@ -73,6 +73,9 @@ int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_des
   if (kv.dtype == Q38A_KV_INT8)
     hipLaunchKernelGGL(attn_decode_kernel<Q38A_KV_INT8>, dim3(grid), dim3(kThreads), 0, stream, a, to_args(b),
                        to_args(kv));
+  else if (kv.dtype == Q38A_KV_INT8_VT)
+    hipLaunchKernelGGL(attn_decode_kernel<Q38A_KV_INT8_VT>, dim3(grid), dim3(kThreads), 0, stream, a, to_args(b),
+                       to_args(kv));
   else
     hipLaunchKernelGGL(attn_decode_kernel<Q38A_KV_BF16>, dim3(grid), dim3(kThreads), 0, stream, a, to_args(b),
                        to_args(kv));

@@ -159,9 +159,11 @@ __device__ inline void softmax_step(const float (&S)[4], const bool (&valid)[4],
   l_run = l_run * corr + psum;
 }
 
-// scale of (token r, group g) from a 32-byte [token][group] fp16 block
+// scale of (token r, group g) from a 32-byte fp16 block, [token][group] (int8 pages) or
+// [group][token] (V scales of int8 VT pages)
+template <bool GroupMajor = false>
 __device__ inline float scale_at(const u32x4 (&sc)[2], int r, int g) {
-  const int idx = r * 4 + g;
+  const int idx = GroupMajor ? g * 4 + r : r * 4 + g;
   const u32x4 w = sc[idx >> 3];
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
   const uint32_t word = ws[(idx & 7) >> 1];
@@ -171,8 +173,9 @@ __device__ inline float scale_at(const u32x4 (&sc)[2], int r, int g) {
 struct Int8Block {
   u32x4 k[4];         // K codes of token t0 + n16, dims 64g + 16 j4 + [0, 16), g = 0..3
   u32x4 ks[2];        // K scales of tokens t0 + 4 j4 + [0, 4): [token][group] fp16
-  uint32_t v[4][4];   // [g][r]: V codes of token t0 + 4 j4 + r, dims 64g + 4 n16 + [0, 4)
-  u32x4 vs[2];        // V scales of tokens t0 + 4 j4 + [0, 4)
+  uint32_t v[4][4];   // int8: [g][r]: V codes of token t0 + 4 j4 + r, dims 64g + 4 n16 + [0, 4)
+                      // VT:   [g][i]: V codes of dim 64g + 16 i + n16, tokens t0 + 4 j4 + [0, 4)
+  u32x4 vs[2];        // V scales of tokens t0 + 4 j4 + [0, 4): [token][group] (int8), [group][token] (VT)
 };
 
 // Per-lane byte offsets of a block's loads, relative to the block's uniform bases (page + 256 *
@@ -181,34 +184,60 @@ struct Int8Offsets {
   uint32_t k, ks, v, vs;
 };
 
+template <bool VT>
 __device__ inline Int8Offsets int8_offsets(const PageLayout& L, int kvh, int n16, int j4) {
   Int8Offsets o;
   o.k = uint32_t(L.k_row(kvh, n16)) + 16 * j4;
   o.ks = uint32_t(L.k_scales(kvh, 4 * j4));
-  o.v = uint32_t(L.v_row(kvh, 4 * j4)) + 4 * n16;
-  o.vs = uint32_t(L.v_scales(kvh, 4 * j4));
+  if constexpr (VT) {
+    o.v = uint32_t(L.vt_code(kvh, n16, 4 * j4));
+    o.vs = uint32_t(L.vt_scale(kvh, 0, 4 * j4));
+  } else {
+    o.v = uint32_t(L.v_row(kvh, 4 * j4)) + 4 * n16;
+    o.vs = uint32_t(L.v_scales(kvh, 4 * j4));
+  }
   return o;
 }
 
-// rows: page + 256 * in0; sc: page + 8 * in0 (in0 = the block's first token within its page)
-__device__ inline void load_int8_block(Int8Block& d, const uint8_t* rows, const uint8_t* sc, const Int8Offsets& o) {
+// pg: the page; in0: the block's first token within it (a multiple of 16). K rows, int8 V rows and
+// VT V^T quarters advance by 256 bytes per token, K and int8 V scales by 8, VT V scales by 2.
+template <bool VT>
+__device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, int in0, const Int8Offsets& o) {
+  const uint8_t* rows = pg + kHeadDim * in0;
+  const uint8_t* sc = pg + 8 * in0;
 #pragma unroll
   for (int g = 0; g < 4; ++g) d.k[g] = *reinterpret_cast<const u32x4*>(rows + o.k + 64 * g);
   d.ks[0] = *reinterpret_cast<const u32x4*>(sc + o.ks);
   d.ks[1] = *reinterpret_cast<const u32x4*>(sc + o.ks + 16);
+  if constexpr (VT) {
+    // one load covers dims 64g + 16i + [0, 16) of the block: 256 contiguous bytes
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) d.v[g][r] = *reinterpret_cast<const uint32_t*>(rows + o.v + kHeadDim * r + 64 * g);
-  d.vs[0] = *reinterpret_cast<const u32x4*>(sc + o.vs);
-  d.vs[1] = *reinterpret_cast<const u32x4*>(sc + o.vs + 16);
+      for (int i = 0; i < 4; ++i)
+        d.v[g][i] = *reinterpret_cast<const uint32_t*>(rows + o.v + 16 * (64 * g + 16 * i));
+    const uint8_t* vsc = pg + 2 * in0 + o.vs;  // group g at + 128 g: 4 tokens = 8 bytes
+    uint2 s[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) s[g] = *reinterpret_cast<const uint2*>(vsc + 2 * kPageTokens * g);
+    d.vs[0] = u32x4{s[0].x, s[0].y, s[1].x, s[1].y};
+    d.vs[1] = u32x4{s[2].x, s[2].y, s[3].x, s[3].y};
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        d.v[g][r] = *reinterpret_cast<const uint32_t*>(rows + o.v + kHeadDim * r + 64 * g);
+    d.vs[0] = *reinterpret_cast<const u32x4*>(sc + o.vs);
+    d.vs[1] = *reinterpret_cast<const u32x4*>(sc + o.vs + 16);
+  }
 }
 
 // One 16-token block of int8 pages for this lane: S^T = K . Q^T per 64-dim group on fp16 MFMAs
 // (codes exact in fp16, q as stored), the group's K scale applied to the fp32 partial; then
 // O += P' V with P' = p * v_scale per group rounded once to fp16 (relative error <= 2^-11; V codes
 // are exact). Tail: the block may reach past the item's last key (masked).
-template <bool Tail>
+template <bool Tail, bool VT = false>
 __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][2], int t0, int t_end, float& m_run,
                                      float& l_run, float4_t (&O)[16], int j4) {
   bool valid[4];
@@ -231,12 +260,19 @@ __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][
   for (int g = 0; g < 4; ++g) {
     half4_t pa;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pa[r] = _Float16(valid[r] ? p[r] * scale_at(d.vs, r, g) : 0.f);
+    for (int r = 0; r < 4; ++r) pa[r] = _Float16(valid[r] ? p[r] * scale_at<VT>(d.vs, r, g) : 0.f);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const half2_t v01 = code_pair_to_half(d.v[g][0], d.v[g][1], i);
-      const half2_t v23 = code_pair_to_half(d.v[g][2], d.v[g][3], i);
-      const half4_t vb = {v01[0], v01[1], v23[0], v23[1]};
+      half4_t vb;
+      if constexpr (VT) {  // the word already holds tokens 0..3 of the lane's dim
+        half2_t lo, hi;
+        codes4_to_half(d.v[g][i], lo, hi);
+        vb = half4_t{lo[0], lo[1], hi[0], hi[1]};
+      } else {  // gather byte i of the four tokens' words
+        const half2_t v01 = code_pair_to_half(d.v[g][0], d.v[g][1], i);
+        const half2_t v23 = code_pair_to_half(d.v[g][2], d.v[g][3], i);
+        vb = half4_t{v01[0], v01[1], v23[0], v23[1]};
+      }
       O[4 * g + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, O[4 * g + i], 0, 0, 0);
     }
   }
@@ -259,6 +295,7 @@ struct BlockSource {
 // computed, and with a claim counter the claim after that is in flight too. Block indices, pages
 // and block-table reads are wave-uniform; blocks past te are masked. The waves of a workgroup do
 // not synchronise here: each loads its q operand straight from global memory.
+template <bool VT>
 __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, int q_row,
                                  const BlockSource& src, float& m_run, float& l_run, float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63;
@@ -280,15 +317,14 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
       }
   }
   const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
-  const Int8Offsets off = int8_offsets(kv.layout, kvh, n16, j4);
+  const Int8Offsets off = int8_offsets<VT>(kv.layout, kvh, n16, j4);
   // the block table is read-only during the launch: through the constant address space its
   // wave-uniform entries become scalar loads, which do not wait behind the vector loads in flight
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
   auto load = [&](Int8Block& d, int idx) {
     const int t0 = src.tb + 16 * idx;
     const uint8_t* pg = layer + size_t(btc[t0 / kPageTokens]) * kv.page_bytes;
-    const int in0 = t0 % kPageTokens;
-    load_int8_block(d, pg + in0 * kHeadDim, pg + in0 * 8, off);
+    load_int8_block<VT>(d, pg, t0 % kPageTokens, off);
   };
   // one lane claims; the value is read (readfirstlane) only when the next block is chosen
   auto claim = [&]() {
@@ -315,7 +351,7 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
     // unconditional (the last iteration reloads the current block): with a single path the
     // compiler's wait for the current block does not also cover the next block's loads
     load(nxt, more ? nidx : idx);
-    compute_block<true>(cur, qf, src.tb + 16 * idx, src.te, m_run, l_run, O, j4);
+    compute_block<true, VT>(cur, qf, src.tb + 16 * idx, src.te, m_run, l_run, O, j4);
     if (!more) break;
     cur = nxt;
     idx = nidx;
@@ -412,9 +448,10 @@ __device__ void decode_item_bf16(const DecodeArgs& a, const KvArgs& kv, const in
   }
 }
 
-// First of the 4 consecutive dims held by accumulator tiles 4 k4 .. 4 k4 + 3 in column n (depends on
-// how V rows were mapped onto MFMA columns): tile k, column n holds dim 64 (k / 4) + 4 n + k % 4 for
-// int8 pages and dim 16 n + k for bf16 pages.
+// Dim held by accumulator tile k in column n (depends on how V was mapped onto MFMA columns): dim
+// 64 (k / 4) + 4 n + k % 4 for int8 pages, 64 (k / 4) + 16 (k % 4) + n for int8 VT pages and
+// 16 n + k for bf16 pages. For int8 and bf16 pages tiles 4 k4 .. 4 k4 + 3 of a column are
+// consecutive dims starting at tile_dim4.
 template <int DT>
 __device__ inline int tile_dim4(int k4, int n) {
   if constexpr (DT == Q38A_KV_INT8) return 64 * k4 + 4 * n;
@@ -452,9 +489,15 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge<W>& sm, int b, int kv
     const int head = 4 * j4 + r;
     if (head < G) {
 #pragma unroll
-      for (int k4 = 0; k4 < 4; ++k4)
-        *reinterpret_cast<float4_t*>(&sm.o[wave][head][tile_dim4<DT>(k4, n16)]) =
-            float4_t{O[4 * k4][r], O[4 * k4 + 1][r], O[4 * k4 + 2][r], O[4 * k4 + 3][r]};
+      for (int k4 = 0; k4 < 4; ++k4) {
+        if constexpr (DT == Q38A_KV_INT8_VT) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sm.o[wave][head][64 * k4 + 16 * i + n16] = O[4 * k4 + i][r];
+        } else {
+          *reinterpret_cast<float4_t*>(&sm.o[wave][head][tile_dim4<DT>(k4, n16)]) =
+              float4_t{O[4 * k4][r], O[4 * k4 + 1][r], O[4 * k4 + 2][r], O[4 * k4 + 3][r]};
+        }
+      }
     }
   }
   __syncthreads();
@@ -521,7 +564,7 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
     float4_t O[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) O[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-    if constexpr (DT == Q38A_KV_INT8) {
+    if constexpr (DT != Q38A_KV_BF16) {
       BlockSource src;
       const int team = split / kTeam, member = split % kTeam;
       const int slot = item - member;  // the team's first item
@@ -540,7 +583,7 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
       }
       src.nblk = ceil_div_i(src.te - src.tb, 16);
       src.stride = W;
-      decode_item_int8(a, kv, bt, kvh, q_row, src, m_run, l_run, O);
+      decode_item_int8<DT == Q38A_KV_INT8_VT>(a, kv, bt, kvh, q_row, src, m_run, l_run, O);
     } else {
       const int t_begin = split * span;
       decode_item_bf16<W>(a, kv, bt, kvh, q_row, t_begin, min(L, t_begin + span), m_run, l_run, O);

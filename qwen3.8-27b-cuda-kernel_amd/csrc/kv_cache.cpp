@@ -92,7 +92,7 @@ int q38a_kv_cache_create(int dtype, int kv_heads, int layers, int num_pages, int
   clear_error();
   if (!out) return set_error(Q38A_ERR_INVALID, "kv_cache_create: out is null");
   *out = nullptr;
-  if ((dtype != Q38A_KV_INT8 && dtype != Q38A_KV_BF16) || kv_heads <= 0 || layers <= 0 || num_pages <= 0 ||
+  if ((dtype != Q38A_KV_INT8 && dtype != Q38A_KV_BF16 && dtype != Q38A_KV_INT8_VT) || kv_heads <= 0 || layers <= 0 || num_pages <= 0 ||
       num_slots <= 0 || max_pages_per_seq <= 0)
     return set_error(Q38A_ERR_INVALID, "kv_cache_create: bad geometry");
   auto* c = new (std::nothrow) q38a_kv_cache();

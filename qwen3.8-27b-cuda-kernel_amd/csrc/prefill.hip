@@ -39,14 +39,17 @@ int launch_attention_prefill(const q38a_attention_params& p, const q38a_batch_de
   int cus = 0;
   if (int rc = device_cu_count(&cus)) return rc;
   const long long units = (static_cast<long long>(b.num_tokens) * G + kRowsPerTile - 1) / kRowsPerTile * p.num_kv_heads;
-  // bf16 pages always: their four-wave form spills (it measured 1.4-1.7x slower at every size)
-  const bool wide = units > cus || kv.dtype == Q38A_KV_BF16;
+  // bf16 and int8 VT pages always: the bf16 four-wave form spills (it measured 1.4-1.7x slower at
+  // every size); the VT staging is written for 512 threads (two per dim)
+  const bool wide = units > cus || kv.dtype != Q38A_KV_INT8;
   const int tiles8 = int((size_t(b.max_tokens_per_seq) * G + 2 * kRowsPerTile - 1) / (2 * kRowsPerTile));
   const dim3 grid8(tiles8 * p.num_kv_heads, b.num_seqs), grid4(tiles_x * p.num_kv_heads, b.num_seqs);
   if (kv.dtype == Q38A_KV_INT8 && wide)
     hipLaunchKernelGGL(attn_prefill8_kernel<Q38A_KV_INT8>, grid8, dim3(2 * kPThreads), 0, stream, a, to_args(b), to_args(kv));
   else if (kv.dtype == Q38A_KV_INT8)
     hipLaunchKernelGGL(attn_prefill_kernel<Q38A_KV_INT8>, grid4, dim3(kPThreads), 0, stream, a, to_args(b), to_args(kv));
+  else if (kv.dtype == Q38A_KV_INT8_VT)
+    hipLaunchKernelGGL(attn_prefill8_kernel<Q38A_KV_INT8_VT>, grid8, dim3(2 * kPThreads), 0, stream, a, to_args(b), to_args(kv));
   else
     hipLaunchKernelGGL(attn_prefill8_kernel<Q38A_KV_BF16>, grid8, dim3(2 * kPThreads), 0, stream, a, to_args(b), to_args(kv));
   return check_hip(hipGetLastError(), "attention_prefill launch");

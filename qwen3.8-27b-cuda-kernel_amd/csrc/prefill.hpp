@@ -49,6 +49,10 @@ static_assert(2 * kRowsPerTile == kPrefillRows, "ragged prefill units are eight-
 // 592, 640 or 656 B, i.e. the dequantising stores are sensitive to the row stride modulo 256.
 constexpr int kKStride = kHeadDim + 8;
 constexpr int kVStride = kHeadDim + 56;
+// int8 VT pages stage V^T: [dim][key] rows of 32 keys (64 B) padded to 80 B; inside each 16-key
+// half the keys are stored in the order 0-3, 8-11, 4-7, 12-15, so the eight keys a lane feeds to
+// one PV MFMA (16 t + 4 kg + [0, 4) and + 8) are one 16-byte read.
+constexpr int kVtStride = kKeyTile + 8;
 constexpr float kRescaleSlack = 8.0f;
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -67,7 +71,10 @@ struct PrefillArgs {
 
 struct alignas(16) KvTile {
   uint16_t k[kKeyTile][kKStride];  // dequantised K, [key][dim]
-  uint16_t v[kKeyTile][kVStride];  // dequantised V, [key][dim]
+  union {
+    uint16_t v[kKeyTile][kVStride];    // dequantised V, [key][dim]
+    uint16_t vt[kHeadDim][kVtStride];  // int8 VT pages: dequantised V^T, [dim][key] (keys permuted)
+  };
 };
 
 // One thread's share of a raw int8 tile in registers: K and V codes of key t % 32, dims
@@ -279,6 +286,69 @@ __device__ inline void store_tile(KvTile& T, const RawTileBf16& R, int key0, int
   bf16_store32(&T.v[key][d0], R.v, live);
 }
 
+// Eight-wave workgroups, int8 VT pages: K as RawTile8 (key t % 32, dims 16 (t / 32) + [0, 16) and
+// its group's scale); V^T of dim t / 2, keys 16 (t % 2) + [0, 16) of the tile (one 16-token quarter:
+// 16 contiguous bytes), and those keys' scales of the dim's group (group-major: 32 contiguous bytes).
+struct RawTileVt8 {
+  u32x4 k;
+  uint16_t ks;
+  u32x4 v;
+  u32x4 vs[2];
+};
+
+struct TileOffsetsVt {
+  int k, ks, v, vs;
+};
+
+__device__ inline TileOffsetsVt tile_offsets_vt8(const PageLayout& L, int kvh, int tid) {
+  TileOffsetsVt o;
+  const int key = tid & 31, slice = tid >> 5;
+  o.k = int(L.k_row(kvh, key)) + 16 * slice;
+  o.ks = int(L.k_scales(kvh, key)) + 2 * (slice >> 2);
+  const int dim = tid >> 1, half = tid & 1;
+  o.v = int(L.vt_code(kvh, dim, 16 * half));
+  o.vs = int(L.vt_scale(kvh, dim >> 6, 16 * half));
+  return o;
+}
+
+// in_page: the tile's first token within the page (K rows and V^T quarters advance 256 B per
+// token, K scales 8 B, VT V scales 2 B)
+__device__ inline void load_raw_vt(RawTileVt8& R, __amdgpu_buffer_rsrc_t pg, int in_page, const TileOffsetsVt& o) {
+  R.k = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.k, in_page * kHeadDim, 0));
+  R.ks = __builtin_amdgcn_raw_buffer_load_b16(pg, o.ks, in_page * 8, 0);
+  R.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.v, in_page * kHeadDim, 0));
+  R.vs[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.vs, 2 * in_page, 0));
+  R.vs[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pg, o.vs, 2 * in_page + 16, 0));
+}
+
+__device__ inline void store_tile(KvTile& T, const RawTileVt8& R, int key0, int limit, int tid) {
+  {
+    const int key = tid & 31, d0 = 16 * (tid >> 5);
+    const bool live = key0 + key < limit;
+    dequant_store16(&T.k[key][d0], R.k, live ? __builtin_bit_cast(_Float16, R.ks) : _Float16(0.0f));
+  }
+  // V^T: 16 codes of one dim, each times its own key's scale (zero past the sequence)
+  const int dim = tid >> 1, kb = 16 * (tid & 1);
+  uint32_t out[8];  // keys kb + 2 i, kb + 2 i + 1 as fp16 pairs
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t u = R.v[w] ^ 0x80808080u;
+    const uint32_t sw0 = R.vs[w >> 1][2 * (w & 1)], sw1 = R.vs[w >> 1][2 * (w & 1) + 1];  // scales of keys 4w..4w+3
+    half2_t s01 = __builtin_bit_cast(half2_t, sw0), s23 = __builtin_bit_cast(half2_t, sw1);
+    const int k = key0 + kb + 4 * w;
+    if (k >= limit) s01[0] = _Float16(0.0f);
+    if (k + 1 >= limit) s01[1] = _Float16(0.0f);
+    if (k + 2 >= limit) s23[0] = _Float16(0.0f);
+    if (k + 3 >= limit) s23[1] = _Float16(0.0f);
+    out[2 * w] = __builtin_bit_cast(uint32_t, dequant_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), s01));
+    out[2 * w + 1] = __builtin_bit_cast(uint32_t, dequant_pair(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), s23));
+  }
+  // stored key order 0-3, 8-11, 4-7, 12-15 (8-byte chunks 0, 2, 1, 3)
+  u32x4* d = reinterpret_cast<u32x4*>(&T.vt[dim][kb]);
+  d[0] = u32x4{out[0], out[1], out[4], out[5]};
+  d[1] = u32x4{out[2], out[3], out[6], out[7]};
+}
+
 // Four consecutive keys of one dim from V [key][dim] in LDS: the lanes of each 16-lane group pass
 // the addresses of V[key0 + j / 4][dim0 + 4 (j % 4)] (j = lane % 16) and lane j receives
 // V[key0 + 0..3][dim0 + j].
@@ -350,20 +420,28 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 
   // The next tile's raw bytes are loaded into registers while the current tile is computed from
   // LDS, then dequantised into the other LDS buffer.
-  using Raw = std::conditional_t<DT == Q38A_KV_INT8, std::conditional_t<kWavesWG == 8, RawTile8, RawTile>,
-                                 std::conditional_t<kWavesWG == 8, RawTileBf16x8, RawTileBf16>>;
-  constexpr int kRowBytes = DT == Q38A_KV_INT8 ? kHeadDim : 2 * kHeadDim;
+  constexpr bool kVt = DT == Q38A_KV_INT8_VT;
+  static_assert(!kVt || (kWavesWG == 8 && kLookahead), "int8 VT pages: eight-wave workgroups with lookahead");
+  using Raw = std::conditional_t<
+      kVt, RawTileVt8,
+      std::conditional_t<DT == Q38A_KV_INT8, std::conditional_t<kWavesWG == 8, RawTile8, RawTile>,
+                         std::conditional_t<kWavesWG == 8, RawTileBf16x8, RawTileBf16>>>;
+  constexpr int kRowBytes = DT != Q38A_KV_BF16 ? kHeadDim : 2 * kHeadDim;
   Raw R;
   // page ids through the constant address space: scalar loads, so a tile's page is a scalar base
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
   auto page_ptr = [&](int key0) { return layer + size_t(btc[key0 / kPageTokens]) * kv.page_bytes; };
-  const TileOffsets toff =
-      DT == Q38A_KV_INT8 ? (kWavesWG == 8 ? tile_offsets8(kv.layout, kvh, tid) : tile_offsets(kv.layout, kvh, tid))
-                         : (kWavesWG == 8 ? tile_offsets_bf16x8(kv.layout, kvh, tid) : tile_offsets_bf16(kv.layout, kvh, tid));
+  using Offsets = std::conditional_t<kVt, TileOffsetsVt, TileOffsets>;
+  Offsets toff;
+  if constexpr (kVt) toff = tile_offsets_vt8(kv.layout, kvh, tid);
+  else if constexpr (DT == Q38A_KV_INT8)
+    toff = kWavesWG == 8 ? tile_offsets8(kv.layout, kvh, tid) : tile_offsets(kv.layout, kvh, tid);
+  else toff = kWavesWG == 8 ? tile_offsets_bf16x8(kv.layout, kvh, tid) : tile_offsets_bf16(kv.layout, kvh, tid);
   auto fetch = [&](Raw& RT, int j) {
     if (j < je) {  // uniform
       const int in_page = (j * kKeyTile) % kPageTokens;
-      load_raw(RT, page_rsrc(page_ptr(j * kKeyTile), kv.page_bytes), in_page * kRowBytes, in_page * 8, toff);
+      if constexpr (kVt) load_raw_vt(RT, page_rsrc(page_ptr(j * kKeyTile), kv.page_bytes), in_page, toff);
+      else load_raw(RT, page_rsrc(page_ptr(j * kKeyTile), kv.page_bytes), in_page * kRowBytes, in_page * 8, toff);
     }
   };
   auto compute = [&](const KvTile& T, int key0) {
@@ -442,11 +520,15 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
       constexpr int kVDepth = kWavesWG == 8 ? 3 : 2;
       auto vread = [&](int i) {  // operand i = 8 t + dt
         const int t = i >> 3, dt = i & 7;
-        const int kk = 16 * t + 4 * kg;
-        const int dim0 = 32 * dt + 16 * ((lane >> 4) & 1);
-        const half4_t lo = v_keys4(T, kk, dim0, lane & 15);
-        const half4_t hi = v_keys4(T, kk + 8, dim0, lane & 15);
-        return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        if constexpr (kVt) {  // V^T rows: the lane's eight keys are adjacent (see kVtStride)
+          return *reinterpret_cast<const half8_t*>(&T.vt[32 * dt + (lane & 31)][16 * t + 8 * kg]);
+        } else {
+          const int kk = 16 * t + 4 * kg;
+          const int dim0 = 32 * dt + 16 * ((lane >> 4) & 1);
+          const half4_t lo = v_keys4(T, kk, dim0, lane & 15);
+          const half4_t hi = v_keys4(T, kk + 8, dim0, lane & 15);
+          return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
       };
       // Eight-wave workgroups: a wave issuing its PV MFMAs runs at raised priority, so the other
       // wave of its SIMD (in its softmax or staging) does not delay the MFMA chain (config 3

@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(kRaggedThreads, 1)
       const int parts = parts_of(batch, b, chunk);
       const int tile_r = local / (pa.nkv * parts), rem = local % (pa.nkv * parts);
       const int tile = prefill_tiles(n, pa.group) - 1 - tile_r;
-      prefill_unit<DT, DT == Q38A_KV_INT8, kRaggedWaves>(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts,
+      prefill_unit<DT, DT != Q38A_KV_BF16, kRaggedWaves>(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts,
                                                          parts,
                                                          r.prefill_partials + size_t(u) * kPrefillRows * kPartialRowFloats);
     }
@@ -252,6 +252,9 @@ int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_des
   const dim3 grid(unsigned(pblocks + dgrid));
   if (kv.dtype == Q38A_KV_INT8)
     hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_INT8>, grid, dim3(kRaggedThreads), 0, stream, r, d, pa, to_args(b),
+                       to_args(kv));
+  else if (kv.dtype == Q38A_KV_INT8_VT)
+    hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_INT8_VT>, grid, dim3(kRaggedThreads), 0, stream, r, d, pa, to_args(b),
                        to_args(kv));
   else
     hipLaunchKernelGGL(attn_ragged_kernel<Q38A_KV_BF16>, grid, dim3(kRaggedThreads), 0, stream, r, d, pa, to_args(b),

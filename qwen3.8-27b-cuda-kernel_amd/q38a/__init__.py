@@ -18,6 +18,7 @@ PAGE_TOKENS = 64
 HEAD_DIM = 256
 KV_INT8 = 0
 KV_BF16 = 1
+KV_INT8_VT = 2  # int8 with V transposed per page (V^T [kvh][256][64], V scales [kvh][4][64])
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("Q38A_LIB") or os.path.join(os.path.dirname(_HERE), "lib", "libq38a.so")

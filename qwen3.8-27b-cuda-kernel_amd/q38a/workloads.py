@@ -50,10 +50,14 @@ def random_pool(num_pages, dtype, gen, layers=1, chunk=512):
     for p0 in range(0, layers * num_pages, chunk):
         n = min(chunk, layers * num_pages - p0)
         kv = torch.randn((n, 2, NKV, 64, HD), generator=gen, device="cuda").to(torch.bfloat16).to(torch.float32)
-        if dtype == q38a.KV_INT8:
-            codes, scales = quantize_rows_int8(kv)
-            view[p0:p0 + n, :2 * NKV * 64 * HD] = codes.view(torch.uint8).reshape(n, -1)
-            view[p0:p0 + n, 2 * NKV * 64 * HD:] = scales.view(torch.uint8).reshape(n, -1)
+        if dtype in (q38a.KV_INT8, q38a.KV_INT8_VT):
+            codes, scales = quantize_rows_int8(kv)  # [n][K|V][kvh][64 tok][256], [n][K|V][kvh][64][4]
+            if dtype == q38a.KV_INT8_VT:  # V codes [kvh][4][256][16], V scales [kvh][4][64]
+                vq = codes[:, 1].reshape(n, NKV, 4, 16, HD).transpose(-1, -2).contiguous()
+                codes = torch.stack([codes[:, 0], vq.view(n, NKV, 64, HD)], 1)
+                scales = torch.stack([scales[:, 0], scales[:, 1].transpose(-1, -2).contiguous().view(n, NKV, 64, 4)], 1)
+            view[p0:p0 + n, :2 * NKV * 64 * HD] = codes.contiguous().view(torch.uint8).reshape(n, -1)
+            view[p0:p0 + n, 2 * NKV * 64 * HD:] = scales.contiguous().view(torch.uint8).reshape(n, -1)
         else:
             view[p0:p0 + n] = kv.to(torch.bfloat16).view(torch.uint8).reshape(n, -1)
     return pool
@@ -109,7 +113,7 @@ class DecodeBatch:
 
     def kv_bytes(self):
         """Algorithmic KV bytes one decode step reads: every key/value of [0, ctx] once."""
-        per = INT8_TOKEN_BYTES if self.dtype == q38a.KV_INT8 else BF16_TOKEN_BYTES
+        per = BF16_TOKEN_BYTES if self.dtype == q38a.KV_BF16 else INT8_TOKEN_BYTES
         return sum(c + 1 for c in self.ctxs) * per
 
     def io_bytes(self):
@@ -183,5 +187,5 @@ class RaggedBatch:
         return prefill_flops([(p, n) for p, n in self.seqs if n > 1])
 
     def decode_kv_bytes(self):
-        per = INT8_TOKEN_BYTES if self.dtype == q38a.KV_INT8 else BF16_TOKEN_BYTES
+        per = BF16_TOKEN_BYTES if self.dtype == q38a.KV_BF16 else INT8_TOKEN_BYTES
         return sum(p + 1 for p, n in self.seqs if n == 1) * per

@@ -36,7 +36,7 @@ def run_append(orc, seqs, kv_dtype, rng, layers=1, layer=0, proj=None, max_pos=N
     return host(q_t, np.uint16).reshape(b.M, NQ, HD), q_ref, pool.download(layer), ref_pool, pool
 
 
-@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16])
+@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16, q38a.KV_INT8_VT])
 def test_append_ragged_bitwise(orc, kv_dtype):
     rng = np.random.default_rng(100 + kv_dtype)
     # prefill chunks that start mid-page and cross pages, decode rows at page edges

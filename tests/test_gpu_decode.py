@@ -81,7 +81,7 @@ def decode_step(orc, ctxs, kv_dtype, seed, max_splits=64, check_pool=True, bt_ov
     return check_close(got, want, what=f"decode ctxs={ctxs} dtype={kv_dtype}")
 
 
-@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16])
+@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16, q38a.KV_INT8_VT])
 def test_decode_page_edges(orc, kv_dtype):
     # contexts around page boundaries, plus the config-1 shape (context 130)
     decode_step(orc, [0, 1, 62, 63, 64, 65, 127, 128, 130, 300, 2100], kv_dtype, seed=1)
@@ -92,7 +92,7 @@ def test_decode_config1_plumbing(orc):
     decode_step(orc, [130], q38a.KV_INT8, seed=0)
 
 
-@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16])
+@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16, q38a.KV_INT8_VT])
 def test_decode_ragged_batch8(orc, kv_dtype):
     rng = np.random.default_rng(2)
     ctxs = [int(x) for x in rng.integers(1024, 8192, 8)]

@@ -63,7 +63,7 @@ def test_prefill_chunks_from_prefixes(orc, prefix):
     prefill_step(orc, [(prefix, 37), (prefix, 64), (prefix, 90), (prefix, 211)], seed=prefix)
 
 
-@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16])
+@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16, q38a.KV_INT8_VT])
 def test_prefill_ragged_batch(orc, kv_dtype):
     """Several sequences of different lengths and prefixes in one launch, incl. a 1-token row."""
     prefill_step(orc, [(0, 130), (500, 1), (777, 300), (64, 64), (2000, 17)], seed=21, kv_dtype=kv_dtype)
@@ -82,7 +82,7 @@ def test_prefill_config3_shape(orc):
     prefill_step(orc, [(6000, 2048)], seed=3, check_tokens=[toks])
 
 
-@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16])
+@pytest.mark.parametrize("kv_dtype", [q38a.KV_INT8, q38a.KV_BF16, q38a.KV_INT8_VT])
 def test_prefill_ragged_batch_256_row_tiles(orc, kv_dtype):
     """Enough rows that the launch takes 256-row workgroups (1,556 tokens x 6 heads x 4 kv heads
     / 128 > 256 CUs): ragged lengths, a 1-token row and tiles that end mid-sequence; the oracle

@@ -90,6 +90,13 @@ def test_ragged_only_decode_bf16(orc, kv_dtype):
     ragged_step(orc, [(c, 1) for c in (5, 640, 3000, 129)], seed=33, kv_dtype=kv_dtype)
 
 
+def test_ragged_mixed_int8_vt(orc):
+    """int8 VT pages (V transposed per page): chunks (split and unsplit tiles) and decode rows in one
+    launch, and the same rows through the prefill launch."""
+    ragged_step(orc, [(0, 130), (5000, 1), (777, 300), (20000, 3), (63, 1), (129, 2), (64, 1)], seed=36,
+                kv_dtype=q38a.KV_INT8_VT, compare_split_launches=True)
+
+
 def test_ragged_mixed_bf16(orc):
     """bf16 pages: chunks (split and unsplit tiles) and decode rows in one launch."""
     ragged_step(orc, [(0, 130), (5000, 1), (777, 300), (20000, 3), (63, 1)], seed=35, kv_dtype=q38a.KV_BF16,

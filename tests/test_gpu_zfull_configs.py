@@ -86,5 +86,13 @@ def test_config5b_long_b1(orc, max_splits):
     run_config(orc, decode_contexts("long_b1"), q38a.KV_INT8, max_splits, "decode")
 
 
+def test_config2_decode_b8_int8_vt(orc):
+    run_config(orc, decode_contexts("decode_b8"), q38a.KV_INT8_VT, 256, "decode")
+
+
+def test_config5a_long_b8_int8_vt(orc):
+    run_config(orc, decode_contexts("long_b8"), q38a.KV_INT8_VT, 256, "decode")
+
+
 def test_config5c_long_b8_bf16(orc):
     run_config(orc, decode_contexts("long_b8_bf16"), q38a.KV_BF16, 256, "decode")

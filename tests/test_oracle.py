@@ -145,7 +145,7 @@ def dequant_row(page, kv_dtype, off, soff):
 
 
 def orc_page_bytes(kv_dtype, nkv=NKV):
-    return 2 * nkv * 64 * (256 + 8) if kv_dtype == 0 else 2 * nkv * 64 * 256 * 2
+    return 2 * nkv * 64 * (256 + 8) if kv_dtype in (0, 2) else 2 * nkv * 64 * 256 * 2
 
 
 def test_int8_bytes_recoverable_from_reference_values(orc, ref):
@@ -238,3 +238,52 @@ def test_paging_is_invisible(orc):
         orc.fill_rows(kr, vr, 0, 0, nkv, pool, 0, bt)
         outs.append(orc.attention_ragged(nq, nkv, [0, 1], [0], [L - 1], q16, gate, nq * 256, pool, 0, bt))
     assert np.array_equal(outs[0], outs[1])
+
+
+def int8_page_to_vt(page, nkv=NKV):
+    """The int8 VT layout stated independently of the oracle: the same page with the V code block
+    [kvh][64 tok][256] rearranged to [kvh][4 quarters][256][16 tok] and the V scale block
+    [kvh][64][4] transposed to [kvh][4][64]."""
+    page = page.copy()
+    cb = nkv * 64 * 256
+    v = page[cb:2 * cb].reshape(nkv, 4, 16, 256)
+    page[cb:2 * cb] = np.ascontiguousarray(v.transpose(0, 1, 3, 2)).reshape(-1)
+    s0 = 2 * cb + nkv * 64 * 8
+    vs = page[s0:s0 + nkv * 64 * 8].view(np.uint16).reshape(nkv, 64, 4)
+    page[s0:s0 + nkv * 64 * 8] = np.ascontiguousarray(vs.transpose(0, 2, 1)).reshape(-1).view(np.uint8)
+    return page
+
+
+def test_int8_vt_layout_is_the_transposed_int8_page(orc):
+    """int8 VT pages hold exactly the int8 page's codes and scales, with the V block transposed:
+    fill and append into both formats and compare byte for byte through the transposition; the
+    attention over either pool is bitwise the same."""
+    rng = np.random.default_rng(21)
+    L, pages = 150, 3
+    kr = bf16_bits_to_f32(randn_bf16(rng, (L, NKV, 256)))
+    vr = bf16_bits_to_f32(randn_bf16(rng, (L, NKV, 256)))
+    vr[7, 2, 64:128] = 0.0  # a zero group: scale 0
+    bt = np.array([[2, 0, 1]], np.int32)
+    pb = orc_page_bytes(0)
+    pools = {}
+    for dt in (0, 2):
+        pool = np.zeros(pb * pages, np.uint8)
+        orc.fill_rows(kr, vr, 0, 0, NKV, pool, dt, bt)
+        pools[dt] = pool
+    proj = randn_bf16(np.random.default_rng(5), (2, LD))
+    qn = np.random.default_rng(6).normal(1.0, 0.2, 256).astype(np.float32)
+    kn = np.random.default_rng(7).normal(1.0, 0.2, 256).astype(np.float32)
+    qs = {dt: orc.qk_norm_rope_append(proj, LD, [L, L + 1], [0, 0], [0], qn, kn, NQ, NKV, pools[dt], dt, bt)
+          for dt in (0, 2)}
+    assert np.array_equal(qs[0], qs[2])
+    for p in range(pages):
+        a = pools[0][p * pb:(p + 1) * pb]
+        b = pools[2][p * pb:(p + 1) * pb]
+        assert np.array_equal(int8_page_to_vt(a), b), f"page {p}"
+    gate = randn_bf16(rng, (2, NQ * 256))
+    outs = [orc.attention_ragged(NQ, NKV, [0, 2], [0], [L, L + 1], qs[dt], gate, NQ * 256, pools[dt], dt, bt)
+            for dt in (0, 2)]
+    assert np.array_equal(outs[0], outs[1])
+    k0, v0 = orc.read_back(pools[0], 0, NKV, bt, 0, L + 2)
+    k2, v2 = orc.read_back(pools[2], 2, NKV, bt, 0, L + 2)
+    assert np.array_equal(k0, k2) and np.array_equal(v0, v2)
