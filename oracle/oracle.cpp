@@ -328,4 +328,108 @@ void orc_attention_ragged(int nq, int nkv, int num_seqs, const int* seq_start, c
   }
 }
 
+// ---- BQ weights and the projection GEMMs (reference docs/FORMAT.md 2, src/bq_host.cpp,
+//      src/kernels/qgemm.cu:285-384) --------------------------------------------------------------
+// The file layout, stated from the format description: slab (kb, nb) = 16 k x 64 n, stored
+// nb-major; lane 4g + t owns column 64 nb + 8 j + g (j < 8) and rows 16 kb + 2t + {0, 1, 8, 9};
+// pair q = 2j + h holds rows 16 kb + 2t + 8h + {0, 1}; lo word q / 4 carries the first element's
+// nibble at bit 4 (q % 4) and the second's at bit 16 + 4 (q % 4); bq5 hi word: bit q / bit 16 + q;
+// bq6 hi words q / 8: bits 2 (q % 8) / 16 + 2 (q % 8); scales: 64-column blocks per (nb, group),
+// column 8j + g at entry 8g + j.
+
+// Writes the file planes of W (codes c in [-2^(b-1), 2^(b-1)) [n][k], bf16 scale bits [n][k/64]).
+void orc_bq_pack_file(int bits, int n, int k, const int8_t* codes, const uint16_t* scales, uint8_t* lo, uint8_t* hi,
+                      uint16_t* sc) {
+  const int slabs_k = k / 16;
+  const size_t hb = bits == 5 ? 128 : bits == 6 ? 256 : 0;
+  std::memset(lo, 0, size_t(n) * k / 2);
+  if (hb) std::memset(hi, 0, size_t(n / 64) * slabs_k * hb);
+  for (int row = 0; row < n; ++row)
+    for (int col = 0; col < k; ++col) {
+      const unsigned u = unsigned(int(codes[size_t(row) * k + col]) + (1 << (bits - 1)));
+      const int nb = row / 64, nl = row % 64, j = nl / 8, g = nl % 8;
+      const int kb = col / 16, kl = col % 16, h = kl / 8, t = (kl % 8) / 2, e = kl % 2;
+      const size_t slab = size_t(nb) * slabs_k + kb;
+      const int lane = 4 * g + t, q = 2 * j + h;
+      uint32_t* w = reinterpret_cast<uint32_t*>(lo + slab * 512 + lane * 16) + q / 4;
+      *w |= uint32_t(u & 15u) << (e ? 16 + 4 * (q % 4) : 4 * (q % 4));
+      if (bits == 5) *reinterpret_cast<uint32_t*>(hi + slab * 128 + lane * 4) |= uint32_t((u >> 4) & 1u) << (e ? 16 + q : q);
+      if (bits == 6)
+        reinterpret_cast<uint32_t*>(hi + slab * 256 + lane * 8)[q / 8] |= uint32_t((u >> 4) & 3u) << (e ? 16 + 2 * (q % 8) : 2 * (q % 8));
+    }
+  for (int row = 0; row < n; ++row)
+    for (int gr = 0; gr < k / 64; ++gr) {
+      const int nb = row / 64, nl = row % 64;
+      sc[(size_t(nb) * (k / 64) + gr) * 64 + (nl % 8) * 8 + nl / 8] = scales[size_t(row) * (k / 64) + gr];
+    }
+}
+
+// Dequantised weights W[n][k] = bf16(code * scale) from the file planes (BQView::weight).
+void orc_bq_file_weight(int bits, int n, int k, const uint8_t* lo, const uint8_t* hi, const uint16_t* sc, float* w) {
+  const int slabs_k = k / 16;
+  for (int row = 0; row < n; ++row)
+    for (int col = 0; col < k; ++col) {
+      const int nb = row / 64, nl = row % 64, j = nl / 8, g = nl % 8;
+      const int kb = col / 16, kl = col % 16, h = kl / 8, t = (kl % 8) / 2, e = kl % 2;
+      const size_t slab = size_t(nb) * slabs_k + kb;
+      const int lane = 4 * g + t, q = 2 * j + h;
+      uint32_t word;
+      std::memcpy(&word, lo + slab * 512 + lane * 16 + 4 * (q / 4), 4);
+      unsigned u = (word >> (e ? 16 + 4 * (q % 4) : 4 * (q % 4))) & 15u;
+      if (bits == 5) {
+        std::memcpy(&word, hi + slab * 128 + lane * 4, 4);
+        u |= ((word >> (e ? 16 + q : q)) & 1u) << 4;
+      } else if (bits == 6) {
+        std::memcpy(&word, hi + slab * 256 + lane * 8 + 4 * (q / 8), 4);
+        u |= ((word >> (e ? 16 + 2 * (q % 8) : 2 * (q % 8))) & 3u) << 4;
+      }
+      const int c = int(u) - (1 << (bits - 1));
+      const float s = bf16_to_f32(sc[(size_t(nb) * (k / 64) + col / 64) * 64 + g * 8 + j]);
+      w[size_t(row) * k + col] = round_bf16(float(c) * s);
+    }
+}
+
+// C = A W^T in double over the reference's bf16 weights, then an epilogue (qgemm.cu:285-384):
+//   kind 0 StoreBF16: out bf16 [m][ldo] = bf16(float(C) * rs), rs from partials_in (or 1);
+//   kind 3 StoreF32:  out fp32 [m][ldo] = float(C) * rs;
+//   kind 2 Residual:  residual[m][n] += float(C); xbf = bf16(residual); partials_out[m][n/128] =
+//                     sum of squares (double) of the new residual over each 128 columns.
+// a: bf16 bits [m][k]; w: fp32 [n][k].
+void orc_qgemm(const uint16_t* a, int m, const float* w, int n, int k, int kind, void* out, int ldo, int n_store,
+               const float* partials_in, int hidden, float eps, float* residual, uint16_t* xbf, float* partials_out) {
+  std::vector<double> arow(static_cast<size_t>(k));
+  for (int row = 0; row < m; ++row) {
+    for (int i = 0; i < k; ++i) arow[size_t(i)] = bf16_to_f32(a[size_t(row) * k + i]);
+    float rs = 1.0f;
+    if (partials_in) {
+      float ssum = 0.0f;
+      for (int b = 0; b < hidden / 128; ++b) ssum += partials_in[size_t(row) * (hidden / 128) + b];
+      rs = 1.0f / std::sqrt(ssum / float(hidden) + eps);
+    }
+    for (int col = 0; col < n; ++col) {
+      const float* wr = w + size_t(col) * k;
+      double c = 0.0;
+      for (int i = 0; i < k; ++i) c += arow[size_t(i)] * wr[i];
+      if (kind == 2) {
+        float& r = residual[size_t(row) * n + col];
+        r = r + float(c);
+        xbf[size_t(row) * n + col] = f32_to_bf16(r);
+      } else if (col < n_store) {
+        const float y = float(c) * rs;
+        if (kind == 3) static_cast<float*>(out)[size_t(row) * ldo + col] = y;
+        else static_cast<uint16_t*>(out)[size_t(row) * ldo + col] = f32_to_bf16(y);
+      }
+    }
+    if (kind == 2)
+      for (int b = 0; b < n / 128; ++b) {
+        double ss = 0.0;
+        for (int col = 128 * b; col < 128 * b + 128; ++col) {
+          const double x = residual[size_t(row) * n + col];
+          ss += x * x;
+        }
+        partials_out[size_t(row) * (n / 128) + b] = float(ss);
+      }
+  }
+}
+
 }  // extern "C"

@@ -52,6 +52,9 @@ class Oracle:
             "orc_read_back": (None, [_p, _i, _i, _p, _i, _i, _i, _p, _p]),
             "orc_attention_token": (None, [_i, _i, _p, _p, _i, _p, _p, _i, _p]),
             "orc_attention_ragged": (None, [_i, _i, _i, _p, _p, _p, _p, _p, _i, _p, _i, _p, _i, _p]),
+            "orc_bq_pack_file": (None, [_i, _i, _i, _p, _p, _p, _p, _p]),
+            "orc_bq_file_weight": (None, [_i, _i, _i, _p, _p, _p, _p]),
+            "orc_qgemm": (None, [_p, _i, _p, _i, _i, _i, _p, _i, _i, _p, _i, _f, _p, _p, _p]),
         }
         for n, (r, a) in sig.items():
             fn = getattr(L, n)
@@ -142,6 +145,47 @@ class Oracle:
                                     tok_pos.ctypes.data, _ptr(np.ascontiguousarray(q16)),
                                     _ptr(np.ascontiguousarray(gate_rows)), ld_gate, pool.ctypes.data, kv_dtype,
                                     bt.ctypes.data, bt.shape[1], out.ctypes.data)
+        return out
+
+
+    # ---- BQ weights and projection GEMMs -------------------------------------------------------
+    def bq_pack_file(self, bits, codes, scales):
+        """codes int8 [n][k] (signed), scales bf16 bits [n][k/64] -> the reference file planes
+        (lo, hi or None, scales)."""
+        codes = np.ascontiguousarray(codes, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint16)
+        n, k = codes.shape
+        lo = np.zeros(n * k // 2, np.uint8)
+        hb = {4: 0, 5: 128, 6: 256}[bits]
+        hi = np.zeros((n // 64) * (k // 16) * hb, np.uint8) if hb else None
+        sc = np.zeros(n * (k // 64), np.uint16)
+        self.L.orc_bq_pack_file(bits, n, k, codes.ctypes.data, scales.ctypes.data, lo.ctypes.data, _ptr(hi),
+                                sc.ctypes.data)
+        return lo, hi, sc
+
+    def bq_file_weight(self, bits, n, k, lo, hi, sc):
+        w = np.empty((n, k), np.float32)
+        self.L.orc_bq_file_weight(bits, n, k, lo.ctypes.data, _ptr(hi), sc.ctypes.data, w.ctypes.data)
+        return w
+
+    def qgemm(self, a, w, kind=0, n_store=0, partials_in=None, hidden=0, eps=1e-6, residual=None):
+        """a bf16 bits [m][k], w fp32 [n][k]. Returns out (bf16 bits or fp32 [m][n]) or, for the residual
+        epilogue, (residual, xbf, partials_out)."""
+        a = np.ascontiguousarray(a, dtype=np.uint16)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        m, k = a.shape
+        n = w.shape[0]
+        pin = None if partials_in is None else np.ascontiguousarray(partials_in, dtype=np.float32)
+        if kind == 2:
+            res = np.array(residual, dtype=np.float32, copy=True)
+            xbf = np.zeros((m, n), np.uint16)
+            pout = np.zeros((m, n // 128), np.float32)
+            self.L.orc_qgemm(a.ctypes.data, m, w.ctypes.data, n, k, 2, None, n, n, None, 0, eps, res.ctypes.data,
+                             xbf.ctypes.data, pout.ctypes.data)
+            return res, xbf, pout
+        out = np.zeros((m, n), np.float32 if kind == 3 else np.uint16)
+        self.L.orc_qgemm(a.ctypes.data, m, w.ctypes.data, n, k, kind, out.ctypes.data, n, n_store or n, _ptr(pin),
+                         hidden, eps, None, None, None)
         return out
 
 

@@ -19,204 +19,12 @@
 // binades (24 + 2 * 14 <= 53 bits), or whenever the total and the lowest set bit of the squares fit
 // in 53 bits. The kernel checks both (wave reductions) and then uses a tree reduction; otherwise
 // one lane replays the left-to-right double sum from LDS.
-#include "common.hpp"
+#include "append.hpp"
 
-// No multiply-add fusion anywhere in this file: every product and sum rounds on its own, as in the
-// reference's x86-64 build.
-#pragma clang fp contract(off)
+// (append.hpp turns multiply-add contraction off for the whole file.)
 
 namespace q38a {
 namespace {
-
-// Correctly rounded binary32 division and square root, as the reference's IEEE single-precision
-// code computes them: HIP compiles fp32 division and sqrtf to correctly rounded sequences
-// (-fhip-fp32-correctly-rounded-divide-sqrt, clang's default, which the build keeps), at a
-// fraction of the cost of the binary64 operations (the quantiser divides every element).
-#ifdef __FAST_MATH__
-#error "the append must round division and square root correctly: build without fast-math"
-#endif
-__device__ inline float div_rn(float a, float b) { return a / b; }
-__device__ inline float sqrt_rn(float a) { return __builtin_sqrtf(a); }
-
-constexpr int kWavesPerBlock = 4;
-
-__device__ inline int exponent_of(float x) {  // floor(log2|x|) for normal x; -149 for subnormals
-  const uint32_t e = (as_u32(x) >> 23) & 0xffu;
-  return e == 0 ? -149 : int(e) - 127;
-}
-
-// Position of the lowest set bit of a nonzero float: x = odd * 2^lowest_bit_of(x).
-__device__ inline int lowest_bit_of(float x) {
-  const uint32_t b = as_u32(x) & 0x7fffffffu;
-  const uint32_t e = b >> 23, m = b & 0x7fffffu;
-  return e == 0 ? -149 + __builtin_ctz(m) : int(e) - 150 + __builtin_ctz(m | 0x800000u);
-}
-
-// floor(log2 x) for a positive normal double
-__device__ inline int exponent_of_f64(double x) {
-  return int((__builtin_bit_cast(uint64_t, x) >> 52) & 0x7ff) - 1023;
-}
-
-__device__ inline double wave_sum(double v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-struct AppendArgs {
-  const uint16_t* proj;
-  int ld_proj;
-  const float* q_norm;
-  const float* k_norm;
-  float eps;
-  int nq, nkv;
-  uint16_t* q_out;
-  int attn_layer;
-  const float* rope;  // [rope_rows][64]
-  int rope_rows;
-};
-
-// Per-row loads, issued for all of a wave's rows before any row is computed (each row's chain is
-// proj + position, then the RoPE row, then tok_seq -> seq_slot -> block_table for a k or v row).
-struct RowLoads {
-  int m, r, pos;
-  uint2 raw;
-  float4 c4, s4;
-  int page;
-  bool store_ok;
-};
-
-// One (token, head row): norm, RoPE, then the q store or the page-row store, from its loads.
-__device__ inline void append_row(const AppendArgs& p, const KvArgs& kv, double* stage, int lane, const RowLoads& L) {
-  const int m = L.m, r = L.r, pos = L.pos, page = L.page;
-  const bool store_ok = L.store_ok;
-  const uint2 raw = L.raw;
-  const float4 c4 = L.c4, s4 = L.s4;
-  const bool is_q = r < p.nq, is_k = !is_q && r < p.nq + p.nkv;
-  const bool pos_ok = pos >= 0 && pos < p.rope_rows;
-  float x[4] = {bf16_value(uint16_t(raw.x)), bf16_value(uint16_t(raw.x >> 16)), bf16_value(uint16_t(raw.y)),
-                bf16_value(uint16_t(raw.y >> 16))};
-
-  if (is_q || is_k) {
-    // ---- sum of squares, bit-identical to the left-to-right double sum --------------------------
-    int emin = 1 << 20, emax = -(1 << 20), lmin = 1 << 20;
-    double part = 0.0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      part += double(x[e]) * double(x[e]);
-      if (x[e] != 0.0f) {
-        const int ex = exponent_of(x[e]);
-        emin = min(emin, ex);
-        emax = max(emax, ex);
-        lmin = min(lmin, lowest_bit_of(x[e]));
-      }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      emin = min(emin, __shfl_xor(emin, off, 64));
-      emax = max(emax, __shfl_xor(emax, off, 64));
-      lmin = min(lmin, __shfl_xor(lmin, off, 64));
-    }
-    // The tree sum equals the left-to-right sum when every partial sum of either order is exact:
-    // (a) the nonzero magnitudes span at most 14 binades, or (b) all partial sums, multiples of
-    // 2^(2 lmin) no larger than the total (< 2^(H + 1)), fit in 53 bits: H + 1 - 2 lmin <= 53. H
-    // comes from the tree sum itself, with one bit of margin for its own rounding.
-    const double tree = wave_sum(part);
-    double ss;
-    if (emax - emin <= 14 || (tree > 0.0 && exponent_of_f64(tree) + 2 - 2 * lmin <= 53)) {
-      ss = tree;  // exact in any order
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) stage[4 * lane + e] = double(x[e]);  // converted off the serial chain
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      double seq = 0.0;
-      if (lane == 0) {
-        // fma(v, v, seq) = fl(seq + v * v) = fl(seq + fl(v * v)): v is a bf16 value, so v * v is exact
-        // in double and the single rounding is the reference's; one instruction less per element
-        for (int i = 0; i < kHeadDim; ++i) {
-          const double v = stage[i];
-          seq = __builtin_fma(v, v, seq);
-        }
-      }
-      ss = __shfl(seq, 0, 64);
-    }
-    const float mean = float(ss / double(kHeadDim));
-    const float rs = div_rn(1.0f, sqrt_rn(mean + p.eps));
-    const float* w = is_q ? p.q_norm : p.k_norm;
-    const float4 wv = *reinterpret_cast<const float4*>(w + 4 * lane);
-    const float wl[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = (x[e] * rs) * wl[e];
-
-    // ---- partial RoPE: lanes 0-7 own dims 0-31, lanes 8-15 own dims 32-63 -----------------------
-    float partner[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) partner[e] = __shfl_xor(x[e], 8, 64);
-    if (lane < 16 && pos_ok) {
-      const float c[4] = {c4.x, c4.y, c4.z, c4.w}, s[4] = {s4.x, s4.y, s4.z, s4.w};
-      if (lane < 8) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = x[e] * c[e] - partner[e] * s[e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = x[e] * c[e] + partner[e] * s[e];
-      }
-    }
-  }
-
-  if (is_q) {
-    uint16_t h[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) h[e] = pos_ok ? f16_bits(x[e]) : uint16_t(0x7e00u);  // NaN flags a bad position
-    uint2 out;
-    out.x = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
-    out.y = uint32_t(h[2]) | (uint32_t(h[3]) << 16);
-    *reinterpret_cast<uint2*>(p.q_out + (size_t(m) * p.nq + r) * kHeadDim + 4 * lane) = out;
-    return;
-  }
-
-  const int head = is_k ? r - p.nq : r - p.nq - p.nkv;
-  if (!store_ok) return;
-  const int tok = pos % kPageTokens;
-  uint8_t* base = kv.pool + size_t(p.attn_layer) * kv.layer_stride + size_t(page) * kv.page_bytes;
-  const bool vt = !is_k && kv.layout.dtype == Q38A_KV_INT8_VT;  // V codes transposed, scales group-major
-  const size_t row = is_k ? kv.layout.k_row(head, tok) : kv.layout.v_row(head, tok);
-
-  if (kv.layout.dtype == Q38A_KV_BF16) {
-    uint2 out;
-    out.x = uint32_t(bf16_bits(x[0])) | (uint32_t(bf16_bits(x[1])) << 16);
-    out.y = uint32_t(bf16_bits(x[2])) | (uint32_t(bf16_bits(x[3])) << 16);
-    *reinterpret_cast<uint2*>(base + row + 8 * lane) = out;
-    return;
-  }
-
-  // int8: group g = lane / 16 covers dims [64g, 64g + 64)
-  float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  const uint16_t sbits = f16_bits(div_rn(amax, 127.0f));
-  const float scale = f16_value(sbits);
-  uint32_t packed = 0;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float q = 0.0f;
-    if (scale > 0.0f) q = fminf(fmaxf(__builtin_rintf(div_rn(x[e], scale)), -127.0f), 127.0f);
-    packed |= (uint32_t(int32_t(q)) & 0xffu) << (8 * e);
-  }
-  if (vt) {
-    // dim 4 lane + e of this token: byte `tok` of V^T row (head, dim)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) base[kv.layout.vt_code(head, 4 * lane + e, tok)] = uint8_t(packed >> (8 * e));
-    if ((lane & 15) == 0) *reinterpret_cast<uint16_t*>(base + kv.layout.vt_scale(head, lane >> 4, tok)) = sbits;
-    return;
-  }
-  *reinterpret_cast<uint32_t*>(base + row + 4 * lane) = packed;
-  if ((lane & 15) == 0) {
-    const size_t so = is_k ? kv.layout.k_scales(head, tok) : kv.layout.v_scales(head, tok);
-    reinterpret_cast<uint16_t*>(base + so)[lane >> 4] = sbits;
-  }
-}
 
 // kRows consecutive jobs (token-major rows) per wave: with one row per wave, a large launch is a
 // sequence of rounds of resident waves, each waiting out its own dependent-load chain.
@@ -241,24 +49,7 @@ qk_norm_rope_append_kernel(AppendArgs p, BatchArgs batch, KvArgs kv, int jobs) {
     L[j].raw = *reinterpret_cast<const uint2*>(p.proj + size_t(L[j].m) * p.ld_proj + col + 4 * lane);
   }
 #pragma unroll
-  for (int j = 0; j < kRows; ++j) {
-    const int pos = L[j].pos;
-    const bool pos_ok = pos >= 0 && pos < p.rope_rows;
-    L[j].c4 = float4{1.f, 1.f, 1.f, 1.f};
-    L[j].s4 = float4{0.f, 0.f, 0.f, 0.f};
-    if (L[j].r < p.nq + p.nkv && lane < 16 && pos_ok) {  // q and k rows: cos/sin of this lane's dims
-      const float* cs = p.rope + size_t(pos) * kRotaryDim + 4 * (lane & 7);
-      L[j].c4 = *reinterpret_cast<const float4*>(cs);
-      L[j].s4 = *reinterpret_cast<const float4*>(cs + 32);
-    }
-    const int page_idx = pos / kPageTokens;
-    L[j].store_ok = L[j].r >= p.nq && pos_ok && page_idx < kv.max_pages_per_seq;
-    L[j].page = 0;
-    if (L[j].store_ok) {
-      const int slot = batch.seq_slot[batch.tok_seq[L[j].m]];
-      L[j].page = kv.block_table[size_t(slot) * kv.max_pages_per_seq + page_idx];
-    }
-  }
+  for (int j = 0; j < kRows; ++j) row_meta(p, batch, kv, lane, L[j]);
 #pragma unroll
   for (int j = 0; j < kRows; ++j)
     if (job0 + j < jobs) append_row(p, kv, stage[wave], lane, L[j]);

@@ -37,6 +37,11 @@ def test_every_declared_symbol_is_exported():
     missing = [n for n in pr if not hasattr(lib, n)]
     assert not missing, missing
     assert set(probe.EXPORTED) == set(pr)
+    from q38a import gemm
+    gm = declared_functions("q38a_gemm.h")
+    missing = [n for n in gm if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(gemm.EXPORTED) == set(gm)
 
 
 def test_page_layout_matches_reference_format():

@@ -1,0 +1,176 @@
+"""GPU parity of the projection GEMMs (include/q38a_gemm.h) against the oracle: q38a_qgemm with its
+StoreBF16 (folded-norm row scale), StoreF32 and Residual epilogues on BQ4/5/6 weights written in the
+reference's file layout and repacked by the library (reference src/kernels/qgemm.cu:285-384), and
+the in-projection with the fused norm / RoPE / append, which must equal q38a_qgemm followed by
+q38a_qk_norm_rope_append bit for bit (q, K/V bytes and scales, the gate columns of proj).
+
+GEMM outputs are compared with the oracle's double-precision product over the reference's
+bf16(code * scale) weights within |d| <= 1e-2 |ref| + 1e-2 rms(ref): the kernel accumulates in fp32
+and applies each group's scale to the exact code sum instead of rounding every weight to bf16
+first, so it differs from the reference by about one bf16 rounding of the output."""
+import numpy as np
+import pytest
+import torch
+
+import q38a
+from q38a import gemm
+from gpu_util import HD, LD, NKV, NQ, Batch, Pool, append_params, dev, host, paged_layout, rope_dev, stream
+from test_gpu_decode import build_context
+from util import assert_bits_equal, bf16_bits_to_f32, f32_to_bf16_bits, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, want, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    rms = float(np.sqrt(np.mean(want ** 2))) if want.size else 0.0
+    d = np.abs(got - want)
+    bound = 1e-2 * np.abs(want) + 1e-2 * rms
+    assert np.isfinite(got).all(), f"{what}: non-finite"
+    bad = d > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {d.size} outside; worst {float((d - bound).max()):.3g} (rms {rms:.3g})"
+    print(f"{what}: max |d| {float(d.max()):.3g}, rms(ref) {rms:.3g}", flush=True)
+
+
+class Weight:
+    """A random BQ weight [n][k]: codes and bf16 scales, the reference file planes (oracle writer),
+    the library's repack on the device, and the oracle's dequantised fp32 weights."""
+
+    def __init__(self, orc, bits, n, k, seed, scale_lo=0.002, scale_hi=0.05):
+        rng = np.random.default_rng(seed)
+        self.bits, self.n, self.k = bits, n, k
+        codes = rng.integers(-(1 << (bits - 1)), 1 << (bits - 1), (n, k)).astype(np.int8)
+        scales = f32_to_bf16_bits(rng.uniform(scale_lo, scale_hi, (n, k // 64)).astype(np.float32))
+        lo, hi, sc = orc.bq_pack_file(bits, codes, scales)
+        self.w_ref = orc.bq_file_weight(bits, n, k, lo, hi, sc)
+        rlo, rhi, rsc = gemm.repack(bits, n, k, lo, hi, sc)
+        self.t = [dev(rlo), dev(rhi) if rhi is not None else None, dev(rsc)]
+        self.desc = gemm.BQWeight(self.t[0].data_ptr(), self.t[1].data_ptr() if self.t[1] is not None else None,
+                                  self.t[2].data_ptr(), bits, n, k, n)
+
+
+def workspace(m, n, k):
+    pf, nc = gemm.workspace_size(m, n, k)
+    p = torch.zeros(max(pf, 1), dtype=torch.float32, device="cuda")
+    c = torch.zeros(max(nc, 1), dtype=torch.int32, device="cuda")
+    return gemm.GemmWorkspace(p.data_ptr(), pf, c.data_ptr(), nc), (p, c)
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6])
+@pytest.mark.parametrize("m", [1, 8, 33, 100])
+def test_qgemm_store_bf16_folded_norm(orc, bits, m):
+    n, k = 512, 1024
+    w = Weight(orc, bits, n, k, seed=100 + bits)
+    rng = np.random.default_rng(m)
+    a = randn_bf16(rng, (m, k))
+    partials = rng.uniform(50.0, 200.0, (m, k // 128)).astype(np.float32)
+    a_t, p_t = dev(a), dev(partials)
+    out = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    ws, keep = workspace(m, n, k)
+    ep = gemm.GemmEpilogue(gemm.EPI_STORE_BF16, out.data_ptr(), n, 0, None, None, None, p_t.data_ptr(), k, 1e-6)
+    print(f"qgemm bf16: bits={bits} m={m} n={n} k={k}", flush=True)
+    for rep in range(2):  # twice: the split-K counters must be back at zero
+        gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
+        torch.cuda.synchronize()
+        got = bf16_bits_to_f32(host(out, np.uint16)).reshape(m, n)
+        want = bf16_bits_to_f32(orc.qgemm(a, w.w_ref, 0, partials_in=partials, hidden=k))
+        close(got, want, f"bits {bits} m {m} rep {rep}")
+
+
+def test_qgemm_store_f32_and_partial_columns(orc):
+    m, n, k = 20, 768, 512
+    w = Weight(orc, 5, n, k, seed=7)
+    a = randn_bf16(np.random.default_rng(3), (m, k))
+    a_t = dev(a)
+    out = torch.full((m * n,), float("nan"), dtype=torch.float32, device="cuda")
+    ws, keep = workspace(m, n, k)
+    n_store = 700
+    ep = gemm.GemmEpilogue(gemm.EPI_STORE_F32, out.data_ptr(), n, n_store, None, None, None, None, 0, 1e-6)
+    gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
+    torch.cuda.synchronize()
+    got = host(out).reshape(m, n)
+    want = orc.qgemm(a, w.w_ref, 3, n_store=n_store)
+    close(got[:, :n_store], want[:, :n_store], "store f32")
+    assert np.isnan(got[:, n_store:]).all()  # columns past n_store untouched
+
+
+@pytest.mark.parametrize("m", [8, 70])
+def test_qgemm_residual(orc, m):
+    """The o-projection's epilogue: residual += C, xbf = bf16(residual), per-128-column sums of squares."""
+    n, k = 1024, 6144
+    w = Weight(orc, 5, n, k, seed=11)
+    rng = np.random.default_rng(5)
+    a = randn_bf16(rng, (m, k))
+    res0 = rng.standard_normal((m, n)).astype(np.float32) * 4
+    a_t, res_t = dev(a), dev(res0)
+    xbf = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    pout = torch.zeros(m * n // 128, dtype=torch.float32, device="cuda")
+    ws, keep = workspace(m, n, k)
+    ep = gemm.GemmEpilogue(gemm.EPI_RESIDUAL, None, 0, 0, res_t.data_ptr(), xbf.data_ptr(), pout.data_ptr(), None, 0,
+                           1e-6)
+    gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
+    torch.cuda.synchronize()
+    r_want, x_want, p_want = orc.qgemm(a, w.w_ref, 2, residual=res0)
+    close(host(res_t).reshape(m, n), r_want, "residual")
+    close(bf16_bits_to_f32(host(xbf, np.uint16)).reshape(m, n), bf16_bits_to_f32(x_want), "xbf")
+    close(host(pout).reshape(m, n // 128), p_want, "partials_out")
+
+
+class InProj:
+    """The attention in-projection of one layer at the model's shape: W [q | gate | k | v] (14,336 x
+    5,120, bq5), hidden rows a, and a paged cache with prior context for every sequence."""
+
+    def __init__(self, orc, seqs, seed, kv_dtype=q38a.KV_INT8, bits=5):
+        self.orc = orc
+        self.k = 5120
+        self.n = LD
+        self.w = Weight(orc, bits, self.n, self.k, seed=seed, scale_lo=0.0005, scale_hi=0.004)
+        rng = np.random.default_rng(seed + 1)
+        self.seqs, self.kv_dtype = seqs, kv_dtype
+        self.bt, self.pages = paged_layout(rng, [p + n for p, n in seqs])
+        self.pool_host = build_context(orc, rng, [p for p, _ in seqs], kv_dtype, self.bt, self.pages)
+        self.b = Batch([(i, p, n) for i, (p, n) in enumerate(seqs)])
+        self.m = self.b.M
+        self.a = randn_bf16(rng, (self.m, self.k), 3.0)
+        self.partials = rng.uniform(2000.0, 9000.0, (self.m, self.k // 128)).astype(np.float32)
+        self.q_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
+        self.k_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
+        self.a_t, self.p_t = dev(self.a), dev(self.partials)
+        self.qn_t, self.kn_t = dev(self.q_norm), dev(self.k_norm)
+        self.rope_t = rope_dev(max(p + n for p, n in seqs) + 1)
+
+    def run(self, fused):
+        pool = Pool(self.kv_dtype, self.pages, self.bt, fill=self.pool_host)
+        proj = torch.zeros(self.m * LD, dtype=torch.int16, device="cuda")
+        q = torch.zeros(self.m * NQ * HD, dtype=torch.int16, device="cuda")
+        ws, keep = workspace(self.m, self.n, self.k)
+        ep = gemm.GemmEpilogue(gemm.EPI_STORE_BF16, proj.data_ptr(), LD, 0, None, None, None, self.p_t.data_ptr(),
+                               self.k, 1e-6)
+        ap = append_params(proj, self.qn_t, self.kn_t, q, self.rope_t)
+        print(f"in-projection: m={self.m} fused={fused} seqs={self.seqs[:4]}", flush=True)
+        if fused:
+            gemm.qgemm_qkv_append(self.a_t.data_ptr(), self.m, self.w.desc, ep, ws, ap, self.b.desc, pool.desc, stream())
+        else:
+            gemm.qgemm(self.a_t.data_ptr(), self.m, self.w.desc, ep, ws, stream())
+            q38a.qk_norm_rope_append(ap, self.b.desc, pool.desc, stream())
+        torch.cuda.synchronize()
+        return host(proj, np.uint16).reshape(self.m, LD), host(q, np.uint16), pool.download()
+
+
+@pytest.mark.parametrize("seqs", [
+    pytest.param([(130, 1), (5000, 1), (63, 1), (2000, 1), (64, 1), (700, 1), (1, 1), (9000, 1)], id="decode_b8"),
+    pytest.param([(300, 200), (40, 1), (0, 64), (1000, 35)], id="mixed_300"),
+])
+def test_in_projection_fused_append_matches_unfused(orc, seqs):
+    ip = InProj(orc, seqs, seed=21)
+    proj_u, q_u, pool_u = ip.run(fused=False)
+    proj_f, q_f, pool_f = ip.run(fused=True)
+    assert_bits_equal(q_f, q_u, "q fp16")
+    assert_bits_equal(pool_f, pool_u, "pool bytes")
+    gate = slice(NQ * HD, 2 * NQ * HD)
+    assert_bits_equal(proj_f[:, gate], proj_u[:, gate], "gate columns of proj")
+    # the unfused projection against the oracle (every row for small m, 24 rows otherwise)
+    rows = np.arange(ip.m) if ip.m <= 16 else np.linspace(0, ip.m - 1, 24).astype(int)
+    want = orc.qgemm(ip.a[rows], ip.w.w_ref, 0, partials_in=ip.partials[rows], hidden=ip.k)
+    close(bf16_bits_to_f32(proj_u[rows]), bf16_bits_to_f32(want), "in-projection vs oracle")
