@@ -176,6 +176,88 @@ def ragged_config(name, seqs, steps, warmup, pools=3, dtype=0):
             "roof_frac": round(t_roof / (attn_ms * 1e-3), 4)}
 
 
+def random_bq_weight(n, k, bits, gen):
+    """Random weights of the in-projection's shape in the q38a BQ layout, on the device (every byte
+    pattern is a valid code; scales ~ U[0.0005, 0.004] in bf16)."""
+    import torch
+    from q38a import gemm
+    nl, nh, ns = gemm.repacked_bytes(bits, n, k)
+    lo = torch.randint(0, 256, (nl,), dtype=torch.uint8, device="cuda", generator=gen)
+    hi = torch.randint(0, 256, (nh,), dtype=torch.uint8, device="cuda", generator=gen) if nh else None
+    sc = (torch.rand(ns // 2, device="cuda", generator=gen) * 0.0035 + 0.0005).to(torch.bfloat16)
+    keep = (lo, hi, sc)
+    w = gemm.BQWeight(lo.data_ptr(), hi.data_ptr() if hi is not None else None, sc.data_ptr(), bits, n, k, n)
+    return w, keep, nl + nh + ns
+
+
+INPROJ_COPIES = 8  # 8 x 48 MB of weights: more than the 256 MB MALL, as 16 layers' weights are
+
+
+def inproj_setup(name):
+    """The attention layer's in-projection (W [q | gate | k | v] = 14,336 x 5,120, bq5 as the reference
+    model stores it, reference docs/FORMAT.md 1.3) on the decode batch of config 2 (M = 8) or the
+    prefill chunk of config 3 (M = 2,048). Launch i uses weight copy i % INPROJ_COPIES, so weights
+    stream from HBM as a step's different layers do. Returns (gemm(i), gemm + append(i), fused(i),
+    facts)."""
+    import torch
+    import q38a
+    from q38a import gemm
+    from q38a.workloads import LD, DecodeBatch, RaggedBatch, decode_contexts
+    s = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    b = DecodeBatch(decode_contexts("decode_b8"), seed=0) if name.endswith("b8") else RaggedBatch([(6000, 2048)], seed=0)
+    m = b.batch.num_tokens
+    K, bits = 5120, 5
+    ws_ = [random_bq_weight(LD, K, bits, gen) for _ in range(INPROJ_COPIES)]
+    wbytes = ws_[0][2]
+    a = torch.randn((m, K), generator=gen, device="cuda").to(torch.bfloat16)
+    partials = torch.rand((m, K // 128), generator=gen, device="cuda") * 100 + 50
+    pf, nc = gemm.workspace_size(m, LD, K)
+    wsp = torch.zeros(max(pf, 1), dtype=torch.float32, device="cuda")
+    wsc = torch.zeros(max(nc, 1), dtype=torch.int32, device="cuda")
+    ws = gemm.GemmWorkspace(wsp.data_ptr(), pf, wsc.data_ptr(), nc)
+    ep = gemm.GemmEpilogue(gemm.EPI_STORE_BF16, b.proj.data_ptr(), LD, 0, None, None, None, partials.data_ptr(), K,
+                           1e-6)
+    ap, kvd = b.append_params(), b.kv_desc(0)
+    keep = (b, ws_, a, partials, wsp, wsc)
+    W = lambda i: ws_[i % INPROJ_COPIES][0]  # noqa: E731
+    run_gemm = lambda i: gemm.qgemm(a.data_ptr(), m, W(i), ep, ws, s)  # noqa: E731
+    run_unfused = lambda i: (gemm.qgemm(a.data_ptr(), m, W(i), ep, ws, s),  # noqa: E731
+                             q38a.qk_norm_rope_append(ap, b.batch, kvd, s))
+    run_fused = lambda i: gemm.qgemm_qkv_append(a.data_ptr(), m, W(i), ep, ws, ap, b.batch, kvd, s)  # noqa: E731
+    return run_gemm, run_unfused, run_fused, {"m": m, "n": LD, "k": K, "bits": bits, "weight_bytes": wbytes,
+                                              "keep": keep}
+
+
+def inproj_config(name, steps, warmup):
+    """The in-projection (inproj_setup) timed three ways: the GEMM alone, GEMM + append (two
+    launches, proj written and re-read), and the fused launch (q38a_qgemm_qkv_append)."""
+    import torch
+    run_gemm, run_unfused, run_fused, f = inproj_setup(name)
+
+    def timed(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    t_gemm, t_unfused, t_fused = timed(run_gemm), timed(run_unfused), timed(run_fused)
+    m, n, k, wbytes = f["m"], f["n"], f["k"], f["weight_bytes"]
+    flops = 2.0 * m * n * k
+    return {"config": name, "m": m, "n": n, "k": k, "bits": f["bits"], "weight_bytes": wbytes,
+            "weight_copies": INPROJ_COPIES,
+            "gemm_ms": round(t_gemm, 5), "gemm_plus_append_ms": round(t_unfused, 5), "fused_ms": round(t_fused, 5),
+            "gemm_weight_gbs": round(wbytes / (t_gemm * 1e-3) / 1e9, 1),
+            "gemm_tflops": round(flops / (t_gemm * 1e-3) / 1e12, 2),
+            "fused_tflops": round(flops / (t_fused * 1e-3) / 1e12, 2)}
+
+
 def runner_decode_config(steps, warmup, layers=16):
     """Config 2's decode step across all 16 full-attention layers through the native runner
     (include/q38a_runtime.h): one hipGraph per batch bucket (metadata upload + append + decode +
@@ -256,6 +338,8 @@ def profile_workload(name, reps=20):
         ap, kvd = rb.attention_params(), rb.kv_desc(0)
         q38a.qk_norm_rope_append(rb.append_params(), rb.batch, kvd, s)
         run = lambda i: q38a.attention_prefill(ap, rb.batch, kvd, s)  # noqa: E731
+    elif base in ("in_proj_b8", "in_proj_2048"):
+        run, _, _, keep = inproj_setup(base)
     elif base == "mixed":
         rb = RaggedBatch(mixed_seqs(0), dtype=q38a.KV_INT8_VT if vt else q38a.KV_INT8, seed=0, pools=3)
         ap, descs = rb.attention_params(), [rb.kv_desc(i) for i in range(3)]
@@ -552,6 +636,9 @@ def main():
                                                           max(10, args.steps // 2), 3, dtype=q38a.KV_INT8_VT)
     if not only or "runner" in only:
         extra["decode_b8_16_layers_runner"] = runner_decode_config(max(10, args.steps // 5), 3)
+    for name in ("in_proj_b8", "in_proj_2048"):
+        if not only or name in only:
+            extra[name] = inproj_config(name, max(10, args.steps // 5), 3)
     if not only or "prefill_ragged" in only:
         extra["prefill_2048_on_6000_ragged"] = ragged_config("prefill_2048_on_6000_ragged", [(6000, 2048)],
                                                              max(10, args.steps // 5), 3, pools=1)

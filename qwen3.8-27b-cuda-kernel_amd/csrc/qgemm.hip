@@ -27,16 +27,25 @@
 //     bf16 into LDS and the append's per-row code (append.hpp) runs on it, so q/k/v never make the
 //     round trip through proj; gate tiles are stored to proj, where attention reads them.
 #include "append.hpp"
+#include <type_traits>
+
 #include "q38a_gemm.h"
 
 namespace q38a {
 namespace {
 
-constexpr int kGWaves = 4;
-constexpr int kGThreads = 64 * kGWaves;
-constexpr int kNB = 2;                          // 32-column MFMA blocks per wave
-constexpr int kTileN = 32 * kNB * kGWaves;      // 256 columns per workgroup
-constexpr int kEpiFused = 100;                  // epilogue kind of the fused in-projection
+// A workgroup covers 256 columns: 8 waves of one 32-column block for one row block (small M: more
+// waves, each with fewer registers, keep more weight bytes in flight), 4 waves of two blocks for two
+// row blocks (more reuse of each A operand).
+constexpr int kTileN = 256;
+constexpr int kMaxWaves = 8;
+__host__ __device__ constexpr int nb_of(int mb) { return mb == 1 ? 1 : 2; }      // 32-column blocks per wave
+__host__ __device__ constexpr int waves_of(int mb) { return kTileN / (32 * nb_of(mb)); }
+// K parts of a workgroup's slice: one row block runs two sets of 8 waves, each over half the slice's
+// groups (twice the weight bytes in flight per CU), their sums added through LDS
+__host__ __device__ constexpr int kparts_of(int mb) { return mb == 1 ? 2 : 1; }
+__host__ __device__ constexpr int threads_of(int mb) { return 64 * waves_of(mb) * kparts_of(mb); }
+constexpr int kEpiFused = 100;  // epilogue kind of the fused in-projection
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -66,129 +75,113 @@ struct GemmArgs {
 struct BWords {
   u32x4 lo;
   u32x2 hi;
-  float scale;
+  uint32_t scale;  // bf16 bits in the low half (converted where used, so the load is not awaited early)
+};
+
+// Buffer resources over the three weight planes: the per-group offsets are wave-uniform (scalar
+// offsets), the lane's part a fixed vector offset, so no per-load 64-bit address arithmetic.
+struct BPlanes {
+  __amdgpu_buffer_rsrc_t lo, hi, sc;
 };
 
 template <int BITS>
-__device__ inline void load_bwords(BWords& b, const GemmArgs& a, int nb, int g, int G, int lane) {
-  const size_t unit = size_t(nb) * G + g;
-  b.lo = *reinterpret_cast<const u32x4*>(a.lo + (unit * 64 + lane) * 16);
-  if constexpr (BITS == 5) b.hi = u32x2{*reinterpret_cast<const uint32_t*>(a.hi + (unit * 64 + lane) * 4), 0u};
-  else if constexpr (BITS == 6) b.hi = *reinterpret_cast<const u32x2*>(a.hi + (unit * 64 + lane) * 8);
-  else b.hi = u32x2{0u, 0u};
-  b.scale = bf16_value(a.scales[unit * 32 + (lane & 31)]);
+__device__ inline BPlanes make_bplanes(const GemmArgs& a) {
+  const int units = (a.n / 32) * (a.k / 64);
+  constexpr int hb = BITS == 4 ? 0 : BITS == 5 ? 4 : 8;
+  BPlanes p;
+  p.lo = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.lo), short(0), units * 1024, 0x00020000);
+  p.hi = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(BITS == 4 ? a.lo : a.hi), short(0), units * 64 * hb,
+                                           0x00020000);
+  p.sc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.scales), short(0), units * 64, 0x00020000);
+  return p;
 }
 
-// B operand of step s: eight bf16 values 128 + u (pairs p = 0..3 of word s), exact.
 template <int BITS>
-__device__ inline bf16x8_t b_operand(const BWords& b, int s) {
-  u32x4 v;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    uint32_t w = ((b.lo[s] >> (4 * p)) & 0x000F000Fu) | 0x43004300u;
-    const int q = 4 * s + p;
-    if constexpr (BITS == 5) w |= ((b.hi.x >> q) << 4) & 0x00100010u;
-    if constexpr (BITS == 6) w |= (((q < 8 ? b.hi.x : b.hi.y) >> (2 * (q & 7))) << 4) & 0x00300030u;
-    v[p] = w;
-  }
+__device__ inline void load_bwords(BWords& b, const BPlanes& p, int nb, int g, int G, int lane) {
+  const int unit = nb * G + g;
+  b.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(p.lo, lane * 16, unit * 1024, 0));
+  if constexpr (BITS == 5) b.hi = u32x2{__builtin_amdgcn_raw_buffer_load_b32(p.hi, lane * 4, unit * 256, 0), 0u};
+  else if constexpr (BITS == 6)
+    b.hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(p.hi, lane * 8, unit * 512, 0));
+  else b.hi = u32x2{0u, 0u};
+  b.scale = __builtin_amdgcn_raw_buffer_load_b16(p.sc, (lane & 31) * 2, unit * 64, 0);
+}
+
+// (x & m) | c in one instruction (v_and_or_b32; m and c wave-uniform)
+__device__ inline uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
+  return r;
+}
+
+// Shift right by a signed constant (left when negative).
+template <int R>
+__device__ inline uint32_t shr(uint32_t x) {
+  if constexpr (R > 0) return x >> R;
+  else if constexpr (R < 0) return x << (-R);
+  else return x;
+}
+
+// Pair P of step S of the B operand: two bf16 values 128 + u, exact: the low nibbles masked into
+// the magic 0x4300 (one shift and one and-or; no shift at P = 0), the high bits masked in at bit 4.
+template <int BITS, int S, int P>
+__device__ inline uint32_t b_pair(const BWords& b, uint32_t magic) {
+  constexpr int q = 4 * S + P;
+  uint32_t w = and_or(shr<4 * P>(b.lo[S]), 0x000F000Fu, magic);
+  if constexpr (BITS == 5) w = and_or(shr<q - 4>(b.hi.x), 0x00100010u, w);
+  if constexpr (BITS == 6) w = and_or(shr<2 * (q & 7) - 4>(q < 8 ? b.hi.x : b.hi.y), 0x00300030u, w);
+  return w;
+}
+
+template <int BITS, int S>
+__device__ inline bf16x8_t b_operand(const BWords& b, uint32_t magic) {
+  const u32x4 v{b_pair<BITS, S, 0>(b, magic), b_pair<BITS, S, 1>(b, magic), b_pair<BITS, S, 2>(b, magic),
+                b_pair<BITS, S, 3>(b, magic)};
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// Row scale of the folded RMSNorm (reference qgemm.cu:288-297).
+// Row scale of the folded RMSNorm (reference qgemm.cu:288-297): 64 partials of the row in flight
+// per round (loads past the row's end re-read its last block and are not added), summed in block
+// order.
 __device__ inline float row_scale(const GemmArgs& a, int row) {
   if (!a.partials_in || row >= a.m) return 1.0f;
   const float* pr = a.partials_in + size_t(row) * a.norm_blocks;
+  const int last = a.norm_blocks - 1;
   float s = 0.0f;
-  for (int b = 0; b < a.norm_blocks; ++b) s += pr[b];
+  for (int b = 0; b < a.norm_blocks; b += 64) {
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) v[i] = pr[b + i < last ? b + i : last];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) s = b + i <= last ? s + v[i] : s;
+  }
   return 1.0f / __builtin_sqrtf(s * a.inv_hidden + a.eps);
 }
 
 struct alignas(16) GemmShared {
   union {
     uint16_t tile[64][kTileN + 8];  // fused epilogue: the bf16 head tile (rows x 256)
-    float resid_ss[kGWaves][64][2];  // residual epilogue: per-wave sums of squares of 64 columns
+    float resid_ss[kMaxWaves][64];  // residual epilogue: per-wave sums of squares of its columns
+    float kpart[kMaxWaves][16][64];  // the second K part's sums (one row block, one column block)
   };
-  double stage[kGWaves][kHeadDim];  // the append's sequential-sum fallback
+  double stage[kMaxWaves][kHeadDim];  // the append's sequential-sum fallback
+  float rs[64];                       // row scales of the folded RMSNorm (1 without partials_in)
   int last;
 };
 
-// C element e of (row block mb, column block j) in this lane: row 32 mb + 8 (e / 4) + 4 (lane / 32) +
-// e % 4 of the tile, column 64 wave + 32 j + lane % 32.
-template <int BITS, int MB, bool FUSED>
-__global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv) {
-  __shared__ GemmShared sh;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// The tile's end, shared by both kernels: split-K slices summed by the last workgroup to arrive,
+// then the epilogue. C element e of (row block mb, column block j) in this lane: row
+// 32 mb + 8 (e / 4) + 4 (lane / 32) + e % 4 of the tile, column 32 (kNB wave + j) + lane % 32. Every
+// wave of the column tile calls it (K-part waves have ended); sh.rs holds the tile's row scales.
+template <int MB, bool FUSED>
+__device__ void tile_finish(const GemmArgs& a, const AppendArgs& ap, const BatchArgs& batch, const KvArgs& kv,
+                            GemmShared& sh, float16_t (&C)[MB][nb_of(MB)], int tile, int z, int tn, int wave,
+                            int lane) {
+  constexpr int kNB = nb_of(MB), kGWaves = waves_of(MB), kBM = 32 * MB;
   const int kg = lane >> 5;
-  constexpr int kBM = 32 * MB;
-  const int bid = blockIdx.x;
-  const int z = bid % a.splits, tile = bid / a.splits;
-  const int tn = tile % a.tiles_n, tm = tile / a.tiles_n;
-  const int m0 = tm * kBM;
-  const int G = a.k / 64;
-  const int g0 = int((long long)z * G / a.splits), g1 = int((long long)(z + 1) * G / a.splits);
-  const int nb0 = tn * (kTileN / 32) + wave * kNB;  // this wave's first 32-column block
-
-  // A rows of this lane (rows past M read as zero)
-  const uint16_t* arow[MB];
-  bool aok[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int row = m0 + 32 * mb + (lane & 31);
-    aok[mb] = row < a.m;
-    arow[mb] = a.a + size_t(aok[mb] ? row : 0) * a.k + 8 * kg;
-  }
-  float16_t C[MB][kNB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int j = 0; j < kNB; ++j) C[mb][j] = float16_t{};
-  const float c0 = 128.0f + float(1 << (BITS - 1));
-  bf16x8_t ones;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ones[i] = __bf16(1.0f);
-
-  u32x4 A[2][MB][4];
-  BWords B[2][kNB];
-  auto load_group = [&](int buf, int g) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(arow[mb] + 64 * g + 16 * s);
-        A[buf][mb][s] = aok[mb] ? v : u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-    for (int j = 0; j < kNB; ++j) load_bwords<BITS>(B[buf][j], a, nb0 + j, g, G, lane);
-  };
-  if (g0 < g1) load_group(0, g0);
-  for (int g = g0; g < g1; ++g) {
-    const int cur = (g - g0) & 1;
-    if (g + 1 < g1) load_group(cur ^ 1, g + 1);
-    float16_t T[MB][kNB], S[MB];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const bf16x8_t x = __builtin_bit_cast(bf16x8_t, A[cur][mb][s]);
-#pragma unroll
-        for (int j = 0; j < kNB; ++j)
-          T[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, b_operand<BITS>(B[cur][j], s),
-                                                              s == 0 ? float16_t{} : T[mb][j], 0, 0, 0);
-        S[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, ones, s == 0 ? float16_t{} : S[mb], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int j = 0; j < kNB; ++j) {
-        const float sc = B[cur][j].scale;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) C[mb][j][e] = __builtin_fmaf(sc, __builtin_fmaf(-c0, S[mb][e], T[mb][j][e]), C[mb][j][e]);
-      }
-  }
-
+  const int m0 = (tile / a.tiles_n) * kBM;
   auto row_of = [&](int mb, int e) { return m0 + 32 * mb + 8 * (e >> 2) + 4 * kg + (e & 3); };
-  const int colw = tn * kTileN + 64 * wave + (lane & 31);  // + 32 j
+  const int colw = tn * kTileN + 32 * kNB * wave + (lane & 31);  // + 32 j
 
   // ---- split-K: the last of the tile's slices sums them in slice order -------------------------
   if (a.splits > 1) {
@@ -201,7 +194,7 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
         for (int e = 0; e < 16; ++e) {
           const int r = row_of(mb, e) - m0;
           if (m0 + r < a.m)
-            __hip_atomic_store(part + (size_t(z) * kBM + r) * kTileN + 64 * wave + 32 * j + (lane & 31), C[mb][j][e],
+            __hip_atomic_store(part + (size_t(z) * kBM + r) * kTileN + 32 * (kNB * wave + j) + (lane & 31), C[mb][j][e],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     __builtin_amdgcn_s_waitcnt(0);  // the write-through stores have completed
@@ -213,25 +206,51 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
     }
     __syncthreads();
     if (!sh.last) return;
+    // the slices in slice order, this workgroup's own included (its stores have completed), read
+    // with agent-coherent (sc1) buffer loads; kZB slices' loads are issued together (a batch past
+    // the last slice re-reads the last one and discards it)
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        part, short(0), int(size_t(a.splits) * kBM * kTileN * sizeof(float)), 0x00020000);
+    constexpr int kSc1 = 16;  // cache policy bit sc1
+    constexpr int kZB = MB == 1 ? 4 : 2;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int j = 0; j < kNB; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = row_of(mb, e) - m0;
-          float sum = 0.0f;
-          if (m0 + r < a.m) {
-            for (int zz = 0; zz < a.splits; ++zz)
-              sum += zz == z ? C[mb][j][e]
-                             : __hip_atomic_load(part + (size_t(zz) * kBM + r) * kTileN + 64 * wave + 32 * j + (lane & 31),
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-          C[mb][j][e] = sum;
-        }
+        for (int e = 0; e < 16; ++e) C[mb][j][e] = 0.0f;
+    for (int zb = 0; zb < a.splits; zb += kZB) {
+      float V[kZB][MB][kNB][16];
+#pragma unroll
+      for (int q = 0; q < kZB; ++q) {
+        const int zz = zb + q < a.splits ? zb + q : a.splits - 1;
+        const int zoff = zz * kBM * kTileN * int(sizeof(float));
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int j = 0; j < kNB; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int r = row_of(mb, e) - m0;
+              const int off = (r * kTileN + 32 * (kNB * wave + j) + (lane & 31)) * int(sizeof(float));
+              V[q][mb][j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, off, zoff, kSc1));
+            }
+      }
+#pragma unroll
+      for (int q = 0; q < kZB; ++q) {
+        const bool use = zb + q < a.splits;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int j = 0; j < kNB; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) C[mb][j][e] = use ? C[mb][j][e] + V[q][mb][j][e] : C[mb][j][e];
+      }
+    }
   }
 
   // ---- epilogues --------------------------------------------------------------------------------
+  if (a.splits == 1) __syncthreads();  // sh.rs (the split-K path has passed barriers already)
   if constexpr (FUSED) {
     const int head = tn;  // proj column blocks: q heads, gate heads, k heads, v heads
     const int nq = ap.nq, nkv = ap.nkv;
@@ -242,7 +261,7 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) rs[mb][i][r] = row_scale(a, row_of(mb, 4 * i + r));
+        for (int r = 0; r < 4; ++r) rs[mb][i][r] = sh.rs[row_of(mb, 4 * i + r) - m0];
     if (is_gate) {
       uint16_t* out = static_cast<uint16_t*>(a.out);
 #pragma unroll
@@ -263,7 +282,7 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
       for (int j = 0; j < kNB; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          sh.tile[row_of(mb, e) - m0][64 * wave + 32 * j + (lane & 31)] = bf16_bits(C[mb][j][e] * rs[mb][e >> 2][e & 3]);
+          sh.tile[row_of(mb, e) - m0][32 * (kNB * wave + j) + (lane & 31)] = bf16_bits(C[mb][j][e] * rs[mb][e >> 2][e & 3]);
     __syncthreads();
     const int rtype = head < nq ? head : (head < 2 * nq + nkv ? nq + (head - 2 * nq) : nq + nkv + (head - 2 * nq - nkv));
     for (int r = wave; r < kBM && m0 + r < a.m; r += kGWaves) {
@@ -302,7 +321,8 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
               ss[mb][e >> 2][e & 3] += x * x;
             }
           }
-      // 64 columns of this wave per row: reduce over the 32 lanes of each half, then pair waves
+      // 32 kNB columns of this wave per row: reduce over the 32 lanes of each half, then the waves
+      // of each 128-column block in wave order
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -320,16 +340,18 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sh.resid_ss[wave][8 * i + 4 * kg + r][0] = ss[mb][i][r];
+            for (int r = 0; r < 4; ++r) sh.resid_ss[wave][8 * i + 4 * kg + r] = ss[mb][i][r];
         }
         __syncthreads();
-        // 128-column block b = (64 wave) / 128: waves 2b and 2b + 1
+        // 128-column block b: waves b wpb .. b wpb + wpb - 1
+        constexpr int wpb = 4 / kNB;
         if (threadIdx.x < 2 * 32) {
           const int bw = threadIdx.x >> 5, r = threadIdx.x & 31;
           const int row = m0 + 32 * mb + r;
-          if (row < a.m)
-            a.partials_out[size_t(row) * a.norm_blocks + (tn * kTileN) / 128 + bw] =
-                sh.resid_ss[2 * bw][r][0] + sh.resid_ss[2 * bw + 1][r][0];
+          float v = 0.0f;
+#pragma unroll
+          for (int w = 0; w < wpb; ++w) v += sh.resid_ss[wpb * bw + w][r];
+          if (row < a.m) a.partials_out[size_t(row) * a.norm_blocks + (tn * kTileN) / 128 + bw] = v;
         }
       }
       return;
@@ -340,7 +362,7 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) rs[mb][i][r] = row_scale(a, row_of(mb, 4 * i + r));
+        for (int r = 0; r < 4; ++r) rs[mb][i][r] = sh.rs[row_of(mb, 4 * i + r) - m0];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -356,21 +378,294 @@ __global__ void __launch_bounds__(kGThreads) qgemm_kernel(GemmArgs a, AppendArgs
   }
 }
 
-// Split-K plan: enough workgroups to stream the weights at HBM speed (about two per CU), at least
-// four groups per slice.
+// Group compute shared by both kernels: T = A . (128 + u) over the group's four 16-k steps of one
+// column block, with A's steps in registers.
+template <int BITS, int MB>
+__device__ inline void group_products(float16_t (&T)[MB], const u32x4 (&Ab)[MB][4], const BWords& bw,
+                                      uint32_t magic) {
+  auto t_step = [&](auto step) {
+    constexpr int s = decltype(step)::value;
+    const bf16x8_t bo = b_operand<BITS, s>(bw, magic);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      T[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, Ab[mb][s]), bo,
+                                                      s == 0 ? float16_t{} : T[mb], 0, 0, 0);
+  };
+  t_step(std::integral_constant<int, 0>{});
+  t_step(std::integral_constant<int, 1>{});
+  t_step(std::integral_constant<int, 2>{});
+  t_step(std::integral_constant<int, 3>{});
+}
+
+// ---- larger M: 64 x 256 tiles, four waves of 64 x 64 ------------------------------------------
+// A and B stream from global memory, two groups in flight per wave; S_g (the rows' sums over a
+// group) from one more MFMA per step against a ones operand.
+template <int BITS, bool FUSED>
+__global__ void __launch_bounds__(threads_of(2)) __attribute__((amdgpu_waves_per_eu(2)))
+qgemm_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv) {
+  constexpr int MB = 2, kNB = nb_of(MB), kBM = 32 * MB;
+  __shared__ GemmShared sh;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, kg = lane >> 5;
+  const int z = blockIdx.x % a.splits, tile = blockIdx.x / a.splits;
+  const int tn = tile % a.tiles_n, m0 = (tile / a.tiles_n) * kBM;
+  const int G = a.k / 64;
+  const int g0 = int((long long)z * G / a.splits), g1 = int((long long)(z + 1) * G / a.splits);
+  const int nb0 = tn * (kTileN / 32) + wave * kNB;  // this wave's first 32-column block
+
+  // A rows of this lane through a buffer resource over the tile's valid rows: rows past M fall
+  // outside its range and load as zero without a memory request
+  const int valid_rows = a.m - m0 < kBM ? a.m - m0 : kBM;
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.a) + size_t(m0) * a.k, short(0), valid_rows * a.k * int(sizeof(uint16_t)), 0x00020000);
+  const BPlanes bp = make_bplanes<BITS>(a);
+  int aoff[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) aoff[mb] = ((32 * mb + (lane & 31)) * a.k + 8 * kg) * int(sizeof(uint16_t));
+  float16_t C[MB][kNB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) C[mb][j] = float16_t{};
+  const float c0 = 128.0f + float(1 << (BITS - 1));
+  const uint32_t magic = 0x43004300u;  // bf16 128 in both halves
+  bf16x8_t ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = __bf16(1.0f);
+
+  // two register buffers rotate over the groups; the rotation loop is unrolled, so every buffer
+  // index is a constant
+  constexpr int kDepth = 2;
+  u32x4 A[kDepth][MB][4];
+  BWords B[kDepth][kNB];
+  auto load_group = [&](u32x4 (&Ab)[MB][4], BWords (&Bb)[kNB], int g) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        Ab[mb][s] =
+            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff[mb], (64 * g + 16 * s) * 2, 0));
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) load_bwords<BITS>(Bb[j], bp, nb0 + j, g, G, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch where it is issued
+  };
+  // compute_group adds a group's products only when `take` (a padded step of the rotation re-reads
+  // the slice's last group and discards it), so the rotation loop has no exits mid-way.
+  auto compute_group = [&](const u32x4 (&Ab)[MB][4], const BWords (&Bb)[kNB], bool take) {
+    float16_t S[MB];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        S[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, Ab[mb][s]), ones,
+                                                        s == 0 ? float16_t{} : S[mb], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kNB; ++j) {
+      float16_t T[MB];
+      group_products<BITS, MB>(T, Ab, Bb[j], magic);
+      // a discarded group adds scale 0 times finite sums (non-finite sums already reached C from the
+      // group's own step)
+      const float sc = take ? bf16_value(uint16_t(Bb[j].scale)) : 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          C[mb][j][e] = __builtin_fmaf(sc, __builtin_fmaf(-c0, S[mb][e], T[mb][e]), C[mb][j][e]);
+    }
+  };
+  // Loads are unconditional (past the slice end they re-read its last group, which is cached): a
+  // load under a branch makes the wait-count bookkeeping assume the worst at the join and wait for
+  // the prefetched groups too. (Every slice holds a group: the host plans splits <= k / 64.)
+  const int glast = g1 - 1;
+  auto gc = [&](int g) { return g < glast ? g : glast; };
+  // the tile's row scales (the epilogue reads them after a barrier): before any weight load is in
+  // flight, as a branch over outstanding loads would make the loop's waits conservative
+  if (threadIdx.x < kBM) sh.rs[threadIdx.x] = row_scale(a, m0 + threadIdx.x);
+#pragma unroll
+  for (int d = 0; d + 1 < kDepth; ++d) load_group(A[d], B[d], gc(g0 + d));
+  for (int g = g0; g < g1; g += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      load_group(A[(d + kDepth - 1) % kDepth], B[(d + kDepth - 1) % kDepth], gc(g + d + kDepth - 1));
+      compute_group(A[d], B[d], g + d < g1);
+    }
+  }
+  tile_finish<MB, FUSED>(a, ap, batch, kv, sh, C, tile, z, tn, wave, lane);
+}
+
+// ---- small M (<= 32 rows): 32 x 256 tiles, sixteen waves ---------------------------------------
+// A decode step's rows are few, so the launch is a stream of weights: per CU as many weight bytes
+// in flight as registers allow. The workgroup's A slice (its rows x the slice's k) and the rows'
+// group sums S_g are staged in LDS once; waves keep only weight words in their register pipeline
+// (kGemvDepth groups deep). Two sets of eight waves (K parts) each cover half the slice's groups
+// for all 256 columns and add their sums through LDS. EV: row quads of the MFMA output that can hold
+// rows < M (1 for M <= 8: the epilogue arithmetic of the other 12 elements is skipped).
+constexpr int kGemvDepth = 6;
+constexpr int kSliceG = 20;                 // most 64-k groups in a workgroup's slice (LDS budget)
+constexpr int kSliceStride = 64 * kSliceG + 8;  // bf16 per staged A row (+16 B against bank conflicts)
+
+constexpr int kMaxNormBlocks = 64;  // folded-norm partials per row (hidden <= 8192)
+constexpr int kStageChunks = (32 * 8 * kSliceG + 1023) / 1024;      // A chunks per thread
+constexpr int kStagePartials = (32 * kMaxNormBlocks + 1023) / 1024;  // partials per thread
+
+struct alignas(16) GemvShared {
+  uint16_t a[32][kSliceStride];  // the tile's A rows over the slice (rows >= M: stale)
+  float s[kSliceG][32];          // S_g per row
+  float p[32 * kMaxNormBlocks];  // the rows' folded-norm partials
+};
+
+template <int BITS, int EV, bool FUSED>
+__global__ void __launch_bounds__(threads_of(1)) __attribute__((amdgpu_waves_per_eu(4)))
+qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv) {
+  constexpr int kKP = kparts_of(1);
+  __shared__ GemmShared sh;
+  __shared__ GemvShared sv;
+  const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wave = hw % waves_of(1), kp = hw / waves_of(1);
+  const int kg = lane >> 5;
+  const int z = blockIdx.x % a.splits, tile = blockIdx.x / a.splits;
+  const int tn = tile % a.tiles_n, m0 = (tile / a.tiles_n) * 32;
+  const int G = a.k / 64;
+  const int gs0 = int((long long)z * G / a.splits), gs1 = int((long long)(z + 1) * G / a.splits);
+  const int gm = gs0 + (gs1 - gs0) / kKP;  // K part 0: [gs0, gm), part 1: [gm, gs1)
+  const int g0 = kp == 0 ? gs0 : gm, g1 = kp == 0 ? gm : gs1;
+  const int nb = tn * (kTileN / 32) + wave;  // this wave's 32-column block
+  const int valid_rows = a.m - m0 < 32 ? a.m - m0 : 32;
+  const BPlanes bp = make_bplanes<BITS>(a);
+
+  // B pipeline first, then the staging loads, so one round trip covers them all; loads past the
+  // part's end re-read its last group (unconditional loads keep the loop's waits exact)
+  BWords B[kGemvDepth];
+  const int glast = g1 - 1;
+  auto gc = [&](int g) { return g < glast ? g : glast; };
+#pragma unroll
+  for (int d = 0; d + 1 < kGemvDepth; ++d) {
+    load_bwords<BITS>(B[d], bp, nb, gc(g0 + d), G, lane);
+    __builtin_amdgcn_sched_barrier(0);  // issue order per group, as in the loop (exact waits there)
+  }
+  // stage the A rows < M over the slice (16-byte chunks; LDS rows >= M keep whatever they hold: an
+  // MFMA output row depends on its A row only, and rows >= M are never stored) and the partials
+  // of the folded norm
+  {
+    const int cpr = 8 * (gs1 - gs0);  // chunks per row
+    const int chunks = valid_rows * cpr;
+    u32x4 v[kStageChunks];
+#pragma unroll
+    for (int i = 0; i < kStageChunks; ++i) {
+      const int c = int(threadIdx.x) + i * threads_of(1), r = c / cpr, kc = c % cpr;
+      if (c < chunks) v[i] = *reinterpret_cast<const u32x4*>(a.a + size_t(m0 + r) * a.k + 64 * gs0 + 8 * kc);
+    }
+    float pv[kStagePartials];
+    const int np = valid_rows * a.norm_blocks;
+#pragma unroll
+    for (int i = 0; i < kStagePartials; ++i) {
+      const int c = int(threadIdx.x) + i * threads_of(1);
+      if (a.partials_in && c < np) pv[i] = a.partials_in[size_t(m0) * a.norm_blocks + c];
+    }
+#pragma unroll
+    for (int i = 0; i < kStageChunks; ++i) {
+      const int c = int(threadIdx.x) + i * threads_of(1), r = c / cpr, kc = c % cpr;
+      if (c < chunks) *reinterpret_cast<u32x4*>(&sv.a[r][8 * kc]) = v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kStagePartials; ++i) {
+      const int c = int(threadIdx.x) + i * threads_of(1);
+      if (a.partials_in && c < np) sv.p[c] = pv[i];
+    }
+    __syncthreads();
+    // row scales (in block order, as row_scale) and group sums S_g (rows >= M: unused)
+    if (threadIdx.x < 32) {
+      float rs = 1.0f;
+      if (a.partials_in && int(threadIdx.x) < valid_rows) {
+        float acc = 0.0f;
+        for (int b = 0; b < a.norm_blocks; ++b) acc += sv.p[threadIdx.x * a.norm_blocks + b];
+        rs = 1.0f / __builtin_sqrtf(acc * a.inv_hidden + a.eps);
+      }
+      sh.rs[threadIdx.x] = rs;
+    }
+    const int ng = gs1 - gs0;
+    for (int t = threadIdx.x; t < 32 * ng; t += threads_of(1)) {
+      const int gl = t >> 5, r = t & 31;
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(&sv.a[r][64 * gl + 8 * c]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc += __builtin_bit_cast(float, w[i] << 16);
+          acc += __builtin_bit_cast(float, w[i] & 0xFFFF0000u);
+        }
+      }
+      sv.s[gl][r] = acc;
+    }
+    __syncthreads();
+  }
+
+  float16_t C[1][1];
+  C[0][0] = float16_t{};
+  const float c0 = 128.0f + float(1 << (BITS - 1));
+  const uint32_t magic = 0x43004300u;
+  const int arow = lane & 31;
+  for (int g = g0; g < g1; g += kGemvDepth) {
+#pragma unroll
+    for (int d = 0; d < kGemvDepth; ++d) {
+      load_bwords<BITS>(B[(d + kGemvDepth - 1) % kGemvDepth], bp, nb, gc(g + d + kGemvDepth - 1), G, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      const int gl = gc(g + d) - gs0;
+      u32x4 Ab[1][4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) Ab[0][s] = *reinterpret_cast<const u32x4*>(&sv.a[arow][64 * gl + 16 * s + 8 * kg]);
+      float16_t T[1];
+      group_products<BITS, 1>(T, Ab, B[d], magic);
+      const float sc = g + d < g1 ? bf16_value(uint16_t(B[d].scale)) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < EV; ++i) {
+        const float4 sq = *reinterpret_cast<const float4*>(&sv.s[gl][8 * i + 4 * kg]);
+        const float sr[4] = {sq.x, sq.y, sq.z, sq.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          C[0][0][4 * i + r] = __builtin_fmaf(sc, __builtin_fmaf(-c0, sr[r], T[0][4 * i + r]), C[0][0][4 * i + r]);
+      }
+    }
+  }
+
+  // part 1 hands its sums to part 0 and ends (barriers count only the waves still running)
+  if (kp == 1) {
+#pragma unroll
+    for (int e = 0; e < 4 * EV; ++e) sh.kpart[wave][e][lane] = C[0][0][e];
+  }
+  __syncthreads();
+  if (kp == 1) return;
+#pragma unroll
+  for (int e = 0; e < 4 * EV; ++e) C[0][0][e] += sh.kpart[wave][e][lane];
+  __syncthreads();  // the union's other uses may overwrite kpart from here on
+  tile_finish<1, FUSED>(a, ap, batch, kv, sh, C, tile, z, tn, wave, lane);
+}
+
+// Split-K plan. Small M (qgemv_kernel, one 1024-thread workgroup per CU): slices of at most
+// kSliceG groups (the staged A), and as many as fill the CUs once without a second round; each of
+// the two K parts keeps a group. Larger M (qgemm_kernel): enough workgroups to stream the weights at
+// HBM speed (about two per CU), at least four groups per slice.
 struct GemmPlan {
   int mb, tiles_m, tiles_n, splits;
 };
 
 GemmPlan plan_gemm(int m, int n, int k, int cus) {
   GemmPlan p;
-  p.mb = m <= 32 ? 1 : 2;
+  const int G = k / 64;
+  p.mb = m <= 32 && G >= 2 ? 1 : 2;
   p.tiles_m = (m + 32 * p.mb - 1) / (32 * p.mb);
   p.tiles_n = n / kTileN;
   const int tiles = p.tiles_m * p.tiles_n;
-  const int G = k / 64;
   int s = 1;
-  while (tiles * s < 2 * cus && G / (2 * s) >= 4 && s < 16) s *= 2;
+  if (p.mb == 1) {
+    const int s_min = (G + kSliceG - 1) / kSliceG, s_fill = cus / tiles;
+    s = s_min > s_fill ? s_min : s_fill;
+    if (s > G / kparts_of(1)) s = G / kparts_of(1);
+    if (s < s_min) s = s_min;  // (G / 2 >= ceil(G / 20) for every G >= 2)
+  } else {
+    while (tiles * s < 2 * cus && G / (2 * s) >= 4 && s < 16) s *= 2;
+  }
   p.splits = s;
   return p;
 }
@@ -398,6 +693,9 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
         size_t(ws.num_counters) < tiles)
       return set_error(Q38A_ERR_INVALID, "qgemm: workspace too small (q38a_qgemm_workspace_size)");
   }
+  if (pl.mb == 1 && ep.partials_in && ep.kind != Q38A_EPI_RESIDUAL && ep.hidden / 128 > kMaxNormBlocks)
+    return set_error(Q38A_ERR_INVALID, "qgemm: hidden %d above %d for the folded norm", ep.hidden,
+                     128 * kMaxNormBlocks);
   GemmArgs g{};
   g.a = A;
   g.m = m;
@@ -413,7 +711,7 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
   g.residual = ep.residual;
   g.xbf = ep.xbf;
   g.partials_out = ep.partials_out;
-  g.partials_in = ep.partials_in;
+  g.partials_in = ep.kind == Q38A_EPI_RESIDUAL ? nullptr : ep.partials_in;  // (the residual epilogue has no row scale)
   g.norm_blocks = ep.kind == Q38A_EPI_RESIDUAL ? w.n / 128 : ep.hidden / 128;
   g.inv_hidden = ep.hidden > 0 ? 1.0f / float(ep.hidden) : 0.0f;
   g.eps = ep.eps;
@@ -430,16 +728,22 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
     ba = to_args(*b);
     ka = to_args(*kv);
   }
-  const dim3 grid(unsigned(pl.tiles_m * pl.tiles_n * pl.splits)), block(kGThreads);
-#define Q38A_QGEMM_LAUNCH(BITS)                                                                            \
-  do {                                                                                                     \
-    if (ap) {                                                                                              \
-      if (pl.mb == 1) hipLaunchKernelGGL((qgemm_kernel<BITS, 1, true>), grid, block, 0, stream, g, aa, ba, ka); \
-      else hipLaunchKernelGGL((qgemm_kernel<BITS, 2, true>), grid, block, 0, stream, g, aa, ba, ka);        \
-    } else {                                                                                               \
-      if (pl.mb == 1) hipLaunchKernelGGL((qgemm_kernel<BITS, 1, false>), grid, block, 0, stream, g, aa, ba, ka); \
-      else hipLaunchKernelGGL((qgemm_kernel<BITS, 2, false>), grid, block, 0, stream, g, aa, ba, ka);       \
-    }                                                                                                      \
+  const dim3 grid(unsigned(pl.tiles_m * pl.tiles_n * pl.splits)), block(unsigned(threads_of(pl.mb)));
+  const bool ev1 = m <= 8;
+#define Q38A_QGEMM_LAUNCH(BITS)                                                                              \
+  do {                                                                                                       \
+    if (pl.mb == 1) {                                                                                        \
+      if (ap) {                                                                                              \
+        if (ev1) hipLaunchKernelGGL((qgemv_kernel<BITS, 1, true>), grid, block, 0, stream, g, aa, ba, ka);   \
+        else hipLaunchKernelGGL((qgemv_kernel<BITS, 4, true>), grid, block, 0, stream, g, aa, ba, ka);       \
+      } else {                                                                                               \
+        if (ev1) hipLaunchKernelGGL((qgemv_kernel<BITS, 1, false>), grid, block, 0, stream, g, aa, ba, ka);  \
+        else hipLaunchKernelGGL((qgemv_kernel<BITS, 4, false>), grid, block, 0, stream, g, aa, ba, ka);      \
+      }                                                                                                      \
+    } else {                                                                                                 \
+      if (ap) hipLaunchKernelGGL((qgemm_kernel<BITS, true>), grid, block, 0, stream, g, aa, ba, ka);         \
+      else hipLaunchKernelGGL((qgemm_kernel<BITS, false>), grid, block, 0, stream, g, aa, ba, ka);           \
+    }                                                                                                        \
   } while (0)
   switch (w.bits) {
     case 4: Q38A_QGEMM_LAUNCH(4); break;
