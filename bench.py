@@ -258,6 +258,66 @@ def inproj_config(name, steps, warmup):
             "fused_tflops": round(flops / (t_fused * 1e-3) / 1e12, 2)}
 
 
+OPROJ_COPIES = 14  # 14 x 20 MB of o-projection weights: more than the 256 MB MALL
+
+
+def oproj_config(name, steps, warmup):
+    """The attention layer's tail on a decode step (config 2 contexts for "o_proj_b8", 5a for
+    "o_proj_long_b8"): split attention, then the o-projection (W_o 5,120 x 6,144, bq5) with the
+    residual epilogue. Unfused: q38a_attention_decode (split kernel + merge kernel writing out), then
+    q38a_qgemm on out. Fused: q38a_attention_decode_partials, then q38a_qgemm_merge_oproj (the merge
+    inside the GEMM's A staging). Launch i uses KV pool i % 3 and weight copy i % OPROJ_COPIES."""
+    import torch
+    import q38a
+    from q38a import gemm
+    from q38a.workloads import DecodeBatch, decode_contexts
+    s = torch.cuda.current_stream().cuda_stream
+    ctx_name = "decode_b8" if name == "o_proj_b8" else "long_b8"
+    b = DecodeBatch(decode_contexts(ctx_name), seed=0, pools=3)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    n, K, B = 5120, 6144, b.B
+    ws_ = [random_bq_weight(n, K, 5, gen) for _ in range(OPROJ_COPIES)]
+    res = torch.randn((B, n), generator=gen, device="cuda")
+    xbf = torch.empty((B, n), dtype=torch.bfloat16, device="cuda")
+    pout = torch.empty((B, n // 128), dtype=torch.float32, device="cuda")
+    pf, nc = gemm.workspace_size(B, n, K)
+    wsp = torch.zeros(max(pf, 1), dtype=torch.float32, device="cuda")
+    wsc = torch.zeros(max(nc, 1), dtype=torch.int32, device="cuda")
+    ws = gemm.GemmWorkspace(wsp.data_ptr(), pf, wsc.data_ptr(), nc)
+    ep = gemm.GemmEpilogue(gemm.EPI_RESIDUAL, None, 0, 0, res.data_ptr(), xbf.data_ptr(), pout.data_ptr(), None, 0,
+                           1e-6)
+    ap, descs = b.attention_params(), [b.kv_desc(i) for i in range(3)]
+    q38a.qk_norm_rope_append(b.append_params(), b.batch, descs[0], s)
+
+    def unfused(i):
+        q38a.attention_decode(ap, b.batch, descs[i % 3], s)
+        gemm.qgemm(b.out.data_ptr(), B, ws_[i % OPROJ_COPIES][0], ep, ws, s)
+
+    def fused(i):
+        q38a.attention_decode_partials(ap, b.batch, descs[i % 3], s)
+        gemm.merge_oproj(ap, b.batch, ws_[i % OPROJ_COPIES][0], ep, ws, s)
+
+    def gemm_only(i):
+        gemm.qgemm(b.out.data_ptr(), B, ws_[i % OPROJ_COPIES][0], ep, ws, s)
+
+    def timed(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    t_u, t_f, t_g = timed(unfused), timed(fused), timed(gemm_only)
+    return {"config": name, "B": B, "n": n, "k": K, "bits": 5, "weight_copies": OPROJ_COPIES,
+            "attention_plus_oproj_ms": round(t_u, 5), "fused_merge_oproj_ms": round(t_f, 5),
+            "oproj_gemm_only_ms": round(t_g, 5), "saved_ms": round(t_u - t_f, 5)}
+
+
 def runner_decode_config(steps, warmup, layers=16):
     """Config 2's decode step across all 16 full-attention layers through the native runner
     (include/q38a_runtime.h): one hipGraph per batch bucket (metadata upload + append + decode +
@@ -639,6 +699,9 @@ def main():
     for name in ("in_proj_b8", "in_proj_2048"):
         if not only or name in only:
             extra[name] = inproj_config(name, max(10, args.steps // 5), 3)
+    for name in ("o_proj_b8", "o_proj_long_b8"):
+        if not only or name in only:
+            extra[name] = oproj_config(name, max(10, args.steps // 5), 3)
     if not only or "prefill_ragged" in only:
         extra["prefill_2048_on_6000_ragged"] = ragged_config("prefill_2048_on_6000_ragged", [(6000, 2048)],
                                                              max(10, args.steps // 5), 3, pools=1)

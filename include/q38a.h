@@ -146,6 +146,13 @@ size_t q38a_split_scratch_floats(int rows, int num_q_heads, int max_splits);
 int q38a_attention_decode(const q38a_attention_params* p, const q38a_batch_desc* batch,
                           const q38a_kv_cache_desc* kv, void* stream);
 
+/* The split kernel of q38a_attention_decode alone: the partials go to p->split_scratch and p->out
+ * is not written. Their consumer is q38a_qgemm_merge_oproj (include/q38a_gemm.h), which merges
+ * them inside the o-projection. No counterpart in the reference (its decode launch always runs the
+ * combine kernel, src/kernels/attention_decode.cu:279-296). */
+int q38a_attention_decode_partials(const q38a_attention_params* p, const q38a_batch_desc* batch,
+                                   const q38a_kv_cache_desc* kv, void* stream);
+
 /* q38a_attention_decode without caller scratch: the split partials go to a static device array
  * of q38a_noalloc_scratch_floats() floats (32 MiB, one per GPU, held until the process ends) and
  * p->split_scratch is ignored; the call allocates nothing (no hipMalloc, no library allocation).

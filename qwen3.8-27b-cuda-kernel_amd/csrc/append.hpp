@@ -5,8 +5,8 @@
 
 #include "common.hpp"
 
-// No multiply-add fusion in this code (and in the rest of any file that includes it): every
-// product and sum rounds on its own, as in the reference's x86-64 build.
+// No multiply-add fusion in this code: every product and sum rounds on its own, as in the
+// reference's x86-64 build. (Restored to the default at the end of this header.)
 #pragma clang fp contract(off)
 
 
@@ -226,3 +226,6 @@ __device__ inline void row_meta(const AppendArgs& p, const BatchArgs& batch, con
 
 }  // namespace
 }  // namespace q38a
+
+// the default contraction again for the code of the including file
+#pragma clang fp contract(fast)

@@ -15,6 +15,8 @@ int launch_qk_norm_rope_append(const q38a_qk_norm_rope_params& p, const q38a_bat
                                const q38a_kv_cache_desc& kv, hipStream_t stream);
 int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
                             hipStream_t stream);
+int launch_attention_decode_partials(const q38a_attention_params& p, const q38a_batch_desc& b,
+                                     const q38a_kv_cache_desc& kv, hipStream_t stream);
 int launch_attention_prefill(const q38a_attention_params& p, const q38a_batch_desc& b,
                              const q38a_kv_cache_desc& kv, hipStream_t stream);
 int launch_attention_ragged(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
@@ -218,6 +220,16 @@ int q38a_attention_decode(const q38a_attention_params* p, const q38a_batch_desc*
     return set_error(Q38A_ERR_INVALID, "attention_decode: one token per sequence required (M %d, B %d)",
                      batch->num_tokens, batch->num_seqs);
   return launch_attention_decode(*p, *batch, *kv, static_cast<hipStream_t>(stream));
+}
+
+int q38a_attention_decode_partials(const q38a_attention_params* p, const q38a_batch_desc* batch,
+                                   const q38a_kv_cache_desc* kv, void* stream) {
+  clear_error();
+  if (int rc = validate_attention(p, batch, kv, true)) return rc;
+  if (batch->num_tokens != batch->num_seqs)
+    return set_error(Q38A_ERR_INVALID, "attention_decode_partials: one token per sequence required (M %d, B %d)",
+                     batch->num_tokens, batch->num_seqs);
+  return launch_attention_decode_partials(*p, *batch, *kv, static_cast<hipStream_t>(stream));
 }
 
 int q38a_attention_decode_noalloc(const q38a_attention_params* p, const q38a_batch_desc* batch,

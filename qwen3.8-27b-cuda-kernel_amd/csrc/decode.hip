@@ -31,10 +31,10 @@ struct MergeArgs {
   int target_items;  // the decode launch's plan target: the split count follows from it
 };
 
-// grid (nq, B): combine the item partials of (decode row b, q head); the split count follows from
-// the decode plan, recomputed here from the launch's metadata exactly as the decode kernel made it.
-__global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, BatchArgs batch) {
-  __shared__ MergeShared sh;
+// grid (nq, B), one wave each: combine the item partials of (decode row b, q head); the split count
+// follows from the decode plan, recomputed here from the launch's metadata exactly as the decode
+// kernel made it.
+__global__ void __launch_bounds__(64) attn_merge_kernel(MergeArgs a, BatchArgs batch) {
   const int hq = blockIdx.x, b = blockIdx.y;
   const int L = decode_len(batch, b);
   if (L == 0) return;
@@ -42,8 +42,8 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, 
   const DecodePlan pl = wave_decode_plan(batch, a.nkv, a.max_splits, a.target_items);
   const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), pl.cp);
   const float* src = a.scratch + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
-  merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
-               a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
+  merge_row_quads(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
+                  a.out + (size_t(row) * a.nq + hq) * kHeadDim);
 }
 
 constexpr int kBlocksPerCu = 2;
@@ -60,8 +60,9 @@ int decode_grid(int* grid, int* target_items) {
   return Q38A_OK;
 }
 
-int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
-                            hipStream_t stream) {
+// The split kernel alone: partials into p.split_scratch (p.out untouched).
+int launch_attention_decode_partials(const q38a_attention_params& p, const q38a_batch_desc& b,
+                                     const q38a_kv_cache_desc& kv, hipStream_t stream) {
   if (b.num_seqs == 0) return Q38A_OK;
   if (b.num_seqs >= kMaxSeqs) return set_error(Q38A_ERR_INVALID, "attention_decode: at most %d sequences", kMaxSeqs - 1);
   if (p.max_splits > kMaxMergeSplits)
@@ -79,12 +80,24 @@ int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_des
   else
     hipLaunchKernelGGL(attn_decode_kernel<Q38A_KV_BF16>, dim3(grid), dim3(kThreads), 0, stream, a, to_args(b),
                        to_args(kv));
-  if (int rc = check_hip(hipGetLastError(), "attention_decode launch")) return rc;
+  return check_hip(hipGetLastError(), "attention_decode launch");
+}
+
+// The gated split merge of a launch_attention_decode_partials into p.out.
+int launch_attention_merge(const q38a_attention_params& p, const q38a_batch_desc& b, hipStream_t stream) {
+  if (b.num_seqs == 0) return Q38A_OK;
+  int grid = 0, target = 0;
+  if (int rc = decode_grid(&grid, &target)) return rc;
   MergeArgs m{p.gate,          p.ld_gate,       p.out,       p.num_q_heads, p.num_kv_heads,
               p.num_q_heads / p.num_kv_heads, p.split_scratch, p.max_splits, target};
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(kMergeThreads), 0, stream, m,
-                     to_args(b));
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(64), 0, stream, m, to_args(b));
   return check_hip(hipGetLastError(), "attention merge launch");
+}
+
+int launch_attention_decode(const q38a_attention_params& p, const q38a_batch_desc& b, const q38a_kv_cache_desc& kv,
+                            hipStream_t stream) {
+  if (int rc = launch_attention_decode_partials(p, b, kv, stream)) return rc;
+  return launch_attention_merge(p, b, stream);
 }
 
 // ---- decode without caller scratch --------------------------------------------------------------

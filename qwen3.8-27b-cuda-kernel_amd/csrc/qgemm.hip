@@ -26,12 +26,17 @@
 //   * The fused in-projection tiles are exactly one 256-column head: a q, k or v tile is rounded to
 //     bf16 into LDS and the append's per-row code (append.hpp) runs on it, so q/k/v never make the
 //     round trip through proj; gate tiles are stored to proj, where attention reads them.
-#include "append.hpp"
 #include <type_traits>
 
+#include "append.hpp"
+#include "decode.hpp"
 #include "q38a_gemm.h"
 
 namespace q38a {
+
+int decode_grid(int* grid, int* target_items);
+int launch_attention_merge(const q38a_attention_params& p, const q38a_batch_desc& b, hipStream_t stream);
+
 namespace {
 
 // A workgroup covers 256 columns: 8 waves of one 32-column block for one row block (small M: more
@@ -68,6 +73,14 @@ struct GemmArgs {
   int tiles_n, splits;
   float* ws_partials;
   int* counters;
+};
+
+// The o-projection's A from decode split partials (q38a_qgemm_merge_oproj): A[row][256 h + d] is the
+// gated merge of (decode row, q head h), as the decode launch's merge kernel computes it.
+struct MergeIn {
+  const float* scratch;
+  const uint16_t* gate;
+  int ld_gate, nq, nkv, max_splits, target_items;
 };
 
 // One lane's share of one (32-column block, group) of weights: 32 low nibbles, their high bits, and
@@ -402,7 +415,7 @@ __device__ inline void group_products(float16_t (&T)[MB], const u32x4 (&Ab)[MB][
 // group) from one more MFMA per step against a ones operand.
 template <int BITS, bool FUSED>
 __global__ void __launch_bounds__(threads_of(2)) __attribute__((amdgpu_waves_per_eu(2)))
-qgemm_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv) {
+qgemm_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn) {
   constexpr int MB = 2, kNB = nb_of(MB), kBM = 32 * MB;
   __shared__ GemmShared sh;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -514,9 +527,10 @@ struct alignas(16) GemvShared {
   float p[32 * kMaxNormBlocks];  // the rows' folded-norm partials
 };
 
-template <int BITS, int EV, bool FUSED>
+// MERGE: the staged A is the gated merge of decode split partials (MergeIn) instead of a.a.
+template <int BITS, int EV, bool FUSED, bool MERGE>
 __global__ void __launch_bounds__(threads_of(1)) __attribute__((amdgpu_waves_per_eu(4)))
-qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv) {
+qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn mi) {
   constexpr int kKP = kparts_of(1);
   __shared__ GemmShared sh;
   __shared__ GemvShared sv;
@@ -548,12 +562,30 @@ qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv) {
   // of the folded norm
   {
     const int cpr = 8 * (gs1 - gs0);  // chunks per row
-    const int chunks = valid_rows * cpr;
+    const int chunks = MERGE ? 0 : valid_rows * cpr;
     u32x4 v[kStageChunks];
 #pragma unroll
     for (int i = 0; i < kStageChunks; ++i) {
       const int c = int(threadIdx.x) + i * threads_of(1), r = c / cpr, kc = c % cpr;
       if (c < chunks) v[i] = *reinterpret_cast<const u32x4*>(a.a + size_t(m0 + r) * a.k + 64 * gs0 + 8 * kc);
+    }
+    if constexpr (MERGE) {
+      // four dims of one (row, q head) per step; a row that is not a decode row (n != 1) is zero
+      const DecodePlan pl = wave_decode_plan(batch, mi.nkv, mi.max_splits, mi.target_items);
+      const int qpr = 16 * (gs1 - gs0);  // quads per row
+      for (int c = threadIdx.x; c < valid_rows * qpr; c += threads_of(1)) {
+        const int r = c / qpr, kq = c % qpr, k = 64 * gs0 + 4 * kq;
+        const int h = k / kHeadDim, d = k % kHeadDim, row = m0 + r;
+        const int b = batch.tok_seq[row];
+        const int L = decode_len(batch, b);
+        uint16_t y[4] = {0, 0, 0, 0};
+        if (L > 0)
+          merge_quad(mi.scratch + (size_t(b) * mi.nq + h) * mi.max_splits * (kHeadDim + 2),
+                     ceil_div_i(ceil_div_i(L, kPageTokens), pl.cp), kHeadDim + 2, d,
+                     mi.gate + size_t(row) * mi.ld_gate + h * kHeadDim + d, y);
+        *reinterpret_cast<uint2*>(&sv.a[r][4 * kq]) =
+            uint2{uint32_t(y[0]) | (uint32_t(y[1]) << 16), uint32_t(y[2]) | (uint32_t(y[3]) << 16)};
+      }
     }
     float pv[kStagePartials];
     const int np = valid_rows * a.norm_blocks;
@@ -680,9 +712,31 @@ int gemm_workspace_size(int m, int n, int k, int cus, size_t out[2]) {
   return Q38A_OK;
 }
 
+template <int BITS>
+void launch_bits(const GemmPlan& pl, bool ev1, int mode, dim3 grid, dim3 block, hipStream_t stream, const GemmArgs& g,
+                 const AppendArgs& aa, const BatchArgs& ba, const KvArgs& ka, const MergeIn& mi) {
+  if (pl.mb == 1) {
+    if (mode == 1) {
+      if (ev1) hipLaunchKernelGGL((qgemv_kernel<BITS, 1, true, false>), grid, block, 0, stream, g, aa, ba, ka, mi);
+      else hipLaunchKernelGGL((qgemv_kernel<BITS, 4, true, false>), grid, block, 0, stream, g, aa, ba, ka, mi);
+    } else if (mode == 2) {
+      if (ev1) hipLaunchKernelGGL((qgemv_kernel<BITS, 1, false, true>), grid, block, 0, stream, g, aa, ba, ka, mi);
+      else hipLaunchKernelGGL((qgemv_kernel<BITS, 4, false, true>), grid, block, 0, stream, g, aa, ba, ka, mi);
+    } else {
+      if (ev1) hipLaunchKernelGGL((qgemv_kernel<BITS, 1, false, false>), grid, block, 0, stream, g, aa, ba, ka, mi);
+      else hipLaunchKernelGGL((qgemv_kernel<BITS, 4, false, false>), grid, block, 0, stream, g, aa, ba, ka, mi);
+    }
+  } else {
+    if (mode == 1) hipLaunchKernelGGL((qgemm_kernel<BITS, true>), grid, block, 0, stream, g, aa, ba, ka, mi);
+    else hipLaunchKernelGGL((qgemm_kernel<BITS, false>), grid, block, 0, stream, g, aa, ba, ka, mi);
+  }
+}
+
+// ap: the fused in-projection append; mi: the o-projection's A merged from decode partials (only
+// plans on the small-M kernel: the caller checks gemm_merge_fits). b: the batch of either.
 int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_gemm_epilogue& ep,
                  const q38a_gemm_workspace& ws, const q38a_qk_norm_rope_params* ap, const q38a_batch_desc* b,
-                 const q38a_kv_cache_desc* kv, hipStream_t stream) {
+                 const q38a_kv_cache_desc* kv, const MergeIn* mi, hipStream_t stream) {
   if (m <= 0) return Q38A_OK;
   int cus = 0;
   if (int rc = device_cu_count(&cus)) return rc;
@@ -722,38 +776,31 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
   AppendArgs aa{};
   BatchArgs ba{};
   KvArgs ka{};
+  MergeIn mg{};
   if (ap) {
     aa = AppendArgs{ap->proj, ap->ld_proj, ap->q_norm, ap->k_norm, ap->eps, ap->num_q_heads, ap->num_kv_heads,
                     ap->q_out, ap->attn_layer, ap->rope_cos_sin, ap->rope_rows};
-    ba = to_args(*b);
     ka = to_args(*kv);
+  }
+  if (b) ba = to_args(*b);
+  if (mi) {
+    if (pl.mb != 1) return set_error(Q38A_ERR_INVALID, "qgemm: the merged A needs the small-M kernel");
+    mg = *mi;
   }
   const dim3 grid(unsigned(pl.tiles_m * pl.tiles_n * pl.splits)), block(unsigned(threads_of(pl.mb)));
   const bool ev1 = m <= 8;
-#define Q38A_QGEMM_LAUNCH(BITS)                                                                              \
-  do {                                                                                                       \
-    if (pl.mb == 1) {                                                                                        \
-      if (ap) {                                                                                              \
-        if (ev1) hipLaunchKernelGGL((qgemv_kernel<BITS, 1, true>), grid, block, 0, stream, g, aa, ba, ka);   \
-        else hipLaunchKernelGGL((qgemv_kernel<BITS, 4, true>), grid, block, 0, stream, g, aa, ba, ka);       \
-      } else {                                                                                               \
-        if (ev1) hipLaunchKernelGGL((qgemv_kernel<BITS, 1, false>), grid, block, 0, stream, g, aa, ba, ka);  \
-        else hipLaunchKernelGGL((qgemv_kernel<BITS, 4, false>), grid, block, 0, stream, g, aa, ba, ka);      \
-      }                                                                                                      \
-    } else {                                                                                                 \
-      if (ap) hipLaunchKernelGGL((qgemm_kernel<BITS, true>), grid, block, 0, stream, g, aa, ba, ka);         \
-      else hipLaunchKernelGGL((qgemm_kernel<BITS, false>), grid, block, 0, stream, g, aa, ba, ka);           \
-    }                                                                                                        \
-  } while (0)
+  const int mode = ap ? 1 : mi ? 2 : 0;
   switch (w.bits) {
-    case 4: Q38A_QGEMM_LAUNCH(4); break;
-    case 5: Q38A_QGEMM_LAUNCH(5); break;
-    case 6: Q38A_QGEMM_LAUNCH(6); break;
+    case 4: launch_bits<4>(pl, ev1, mode, grid, block, stream, g, aa, ba, ka, mg); break;
+    case 5: launch_bits<5>(pl, ev1, mode, grid, block, stream, g, aa, ba, ka, mg); break;
+    case 6: launch_bits<6>(pl, ev1, mode, grid, block, stream, g, aa, ba, ka, mg); break;
     default: return set_error(Q38A_ERR_UNSUPPORTED, "qgemm: %d-bit weights are not supported", w.bits);
   }
-#undef Q38A_QGEMM_LAUNCH
   return check_hip(hipGetLastError(), "qgemm launch");
 }
+
+// Whether q38a_qgemm_merge_oproj runs the merge inside the GEMM for m rows (the small-M kernel).
+bool gemm_merge_fits(int m, int n, int k, int cus) { return plan_gemm(m, n, k, cus).mb == 1; }
 
 }  // namespace q38a
 
@@ -802,7 +849,7 @@ int q38a_qgemm(const uint16_t* a, int m, const q38a_bq_weight* w, const q38a_gem
                const q38a_gemm_workspace* ws, void* stream) {
   clear_error();
   if (int rc = validate_gemm(a, m, w, ep, ws)) return rc;
-  return launch_qgemm(a, m, *w, *ep, *ws, nullptr, nullptr, nullptr, static_cast<hipStream_t>(stream));
+  return launch_qgemm(a, m, *w, *ep, *ws, nullptr, nullptr, nullptr, nullptr, static_cast<hipStream_t>(stream));
 }
 
 int q38a_qgemm_qkv_append(const uint16_t* a, int m, const q38a_bq_weight* w, const q38a_gemm_epilogue* ep,
@@ -825,7 +872,36 @@ int q38a_qgemm_qkv_append(const uint16_t* a, int m, const q38a_bq_weight* w, con
     return set_error(Q38A_ERR_INVALID, "qgemm_qkv_append: the epilogue's out/ldo must be the append's proj/ld_proj");
   if (ep->n_store != 0 && ep->n_store != w->n)
     return set_error(Q38A_ERR_INVALID, "qgemm_qkv_append: n_store must cover the whole projection");
-  return launch_qgemm(a, m, *w, *ep, *ws, p, batch, kv, static_cast<hipStream_t>(stream));
+  return launch_qgemm(a, m, *w, *ep, *ws, p, batch, kv, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int q38a_qgemm_merge_oproj(const q38a_attention_params* attn, const q38a_batch_desc* batch, const q38a_bq_weight* w,
+                           const q38a_gemm_epilogue* ep, const q38a_gemm_workspace* ws, void* stream) {
+  clear_error();
+  if (!attn || !batch) return set_error(Q38A_ERR_INVALID, "qgemm_merge_oproj: null argument");
+  if (int rc = validate_gemm(attn->out, batch->num_tokens, w, ep, ws)) return rc;
+  if (int rc = validate_batch(batch, true)) return rc;
+  const int nq = attn->num_q_heads, nkv = attn->num_kv_heads;
+  if (nq <= 0 || nkv <= 0 || nq % nkv || !attn->gate || !attn->split_scratch || attn->max_splits <= 0 ||
+      attn->max_splits > kMaxMergeSplits || attn->ld_gate < nq * kHeadDim)
+    return set_error(Q38A_ERR_INVALID, "qgemm_merge_oproj: attention heads, gate, split scratch or max_splits invalid");
+  if (batch->num_tokens != batch->num_seqs)
+    return set_error(Q38A_ERR_INVALID, "qgemm_merge_oproj: one token per sequence required (M %d, B %d)",
+                     batch->num_tokens, batch->num_seqs);
+  if (w->k != nq * kHeadDim)
+    return set_error(Q38A_ERR_INVALID, "qgemm_merge_oproj: weight k %d != %d q heads x 256", w->k, nq);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int m = batch->num_tokens;
+  int cus = 0, grid = 0, target = 0;
+  if (int rc = device_cu_count(&cus)) return rc;
+  if (int rc = decode_grid(&grid, &target)) return rc;
+  if (!gemm_merge_fits(m, w->n, w->k, cus)) {
+    // larger batches: the merge kernel writes attn->out, which the GEMM reads
+    if (int rc = launch_attention_merge(*attn, *batch, st)) return rc;
+    return launch_qgemm(attn->out, m, *w, *ep, *ws, nullptr, batch, nullptr, nullptr, st);
+  }
+  const MergeIn mi{attn->split_scratch, attn->gate, attn->ld_gate, nq, nkv, attn->max_splits, target};
+  return launch_qgemm(attn->out, m, *w, *ep, *ws, nullptr, batch, nullptr, &mi, st);
 }
 
 }  // extern "C"

@@ -84,6 +84,7 @@ _SIGS = {
     "q38a_split_scratch_floats": (_sz, [_i, _i, _i]),
     "q38a_ragged_scratch_floats": (_sz, [_i, _i, _i, _i, _i, _i]),
     "q38a_attention_decode": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
+    "q38a_attention_decode_partials": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_attention_prefill": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_attention_ragged": (_i, [ctypes.POINTER(AttentionParams), _PBatch, _PKv, _p]),
     "q38a_ragged_scratch_init": (_i, [_p, _p]),
@@ -148,6 +149,11 @@ def qk_norm_rope_append(params, batch, kv, stream=0):
 
 def attention_decode(params, batch, kv, stream=0):
     _check(lib.q38a_attention_decode(ctypes.byref(params), ctypes.byref(batch), ctypes.byref(kv), stream))
+
+
+def attention_decode_partials(params, batch, kv, stream=0):
+    """The decode split kernel alone (partials for q38a_qgemm_merge_oproj; params.out not written)."""
+    _check(lib.q38a_attention_decode_partials(ctypes.byref(params), ctypes.byref(batch), ctypes.byref(kv), stream))
 
 
 def attention_prefill(params, batch, kv, stream=0):

@@ -32,6 +32,8 @@ _SIGS = {
                                    ctypes.POINTER(GemmWorkspace), ctypes.POINTER(QkNormRopeParams),
                                    ctypes.POINTER(BatchDesc), ctypes.POINTER(KvCacheDesc), _p]),
     "q38a_qgemm_workspace_size": (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
+    "q38a_qgemm_merge_oproj": (_i, [ctypes.POINTER(AttentionParams), ctypes.POINTER(BatchDesc), ctypes.POINTER(BQWeight),
+                                    ctypes.POINTER(GemmEpilogue), ctypes.POINTER(GemmWorkspace), _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -70,6 +72,12 @@ def workspace_size(m, n, k):
 
 def qgemm(a_ptr, m, w, ep, ws, stream=0):
     _check(lib.q38a_qgemm(a_ptr, m, ctypes.byref(w), ctypes.byref(ep), ctypes.byref(ws), stream))
+
+
+def merge_oproj(attn, batch, w, ep, ws, stream=0):
+    """The o-projection straight from the decode split partials of attention_decode_partials."""
+    _check(lib.q38a_qgemm_merge_oproj(ctypes.byref(attn), ctypes.byref(batch), ctypes.byref(w), ctypes.byref(ep),
+                                      ctypes.byref(ws), stream))
 
 
 def qgemm_qkv_append(a_ptr, m, w, ep, ws, append, batch, kv, stream=0):

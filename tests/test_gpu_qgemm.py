@@ -174,3 +174,63 @@ def test_in_projection_fused_append_matches_unfused(orc, seqs):
     rows = np.arange(ip.m) if ip.m <= 16 else np.linspace(0, ip.m - 1, 24).astype(int)
     want = orc.qgemm(ip.a[rows], ip.w.w_ref, 0, partials_in=ip.partials[rows], hidden=ip.k)
     close(bf16_bits_to_f32(proj_u[rows]), bf16_bits_to_f32(want), "in-projection vs oracle")
+
+
+@pytest.mark.parametrize("ctxs,n", [
+    pytest.param([130, 5000, 63, 2000, 64, 700, 1, 9000], 5120, id="b8"),
+    pytest.param([20000, 513], 5120, id="b2_long"),
+    pytest.param([40 + 37 * i for i in range(40)], 1024, id="b40_merge_kernel"),
+])
+def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n):
+    """q38a_qgemm_merge_oproj (the merge inside the o-projection's A staging, or for more than 32
+    rows the merge kernel then the GEMM) equals q38a_attention_decode followed by q38a_qgemm on its
+    out, bit for bit in residual, xbf and partials_out; that GEMM against the oracle's."""
+    from gpu_util import attention_params
+    from util import randn_bf16
+    rng = np.random.default_rng(77)
+    B, max_splits = len(ctxs), 64
+    bt, pages = paged_layout(rng, [c + 1 for c in ctxs])
+    pool_host = build_context(orc, rng, ctxs, q38a.KV_INT8, bt, pages)
+    pool = Pool(q38a.KV_INT8, pages, bt, fill=pool_host)
+    b = Batch([(i, c, 1) for i, c in enumerate(ctxs)])
+    proj = randn_bf16(rng, (B, LD))
+    qn = dev(rng.normal(1.0, 0.1, HD).astype(np.float32))
+    kn = dev(rng.normal(1.0, 0.1, HD).astype(np.float32))
+    proj_t = dev(proj)
+    q_t = torch.zeros(B * NQ * HD, dtype=torch.int16, device="cuda")
+    rope_t = rope_dev(max(ctxs) + 1)
+    q38a.qk_norm_rope_append(append_params(proj_t, qn, kn, q_t, rope_t), b.desc, pool.desc, stream())
+    w = Weight(orc, 5, n, NQ * HD, seed=31, scale_lo=0.0005, scale_hi=0.004)
+    res0 = (rng.standard_normal((B, n)) * 4).astype(np.float32)
+    print(f"merge_oproj: B={B} n={n} ctxs={ctxs[:8]}", flush=True)
+
+    def run(fused):
+        out_t = torch.zeros(B * NQ * HD, dtype=torch.int16, device="cuda")
+        scratch_t = torch.full((q38a.split_scratch_floats(B, NQ, max_splits),), float("nan"), dtype=torch.float32,
+                               device="cuda")
+        attn = attention_params(q_t, proj_t, out_t, scratch_t, max_splits)
+        res_t = dev(res0)
+        xbf = torch.zeros(B * n, dtype=torch.int16, device="cuda")
+        pout = torch.zeros(B * n // 128, dtype=torch.float32, device="cuda")
+        ws, keep = workspace(B, n, NQ * HD)
+        ep = gemm.GemmEpilogue(gemm.EPI_RESIDUAL, None, 0, 0, res_t.data_ptr(), xbf.data_ptr(), pout.data_ptr(), None,
+                               0, 1e-6)
+        if fused:
+            q38a.attention_decode_partials(attn, b.desc, pool.desc, stream())
+            gemm.merge_oproj(attn, b.desc, w.desc, ep, ws, stream())
+        else:
+            q38a.attention_decode(attn, b.desc, pool.desc, stream())
+            gemm.qgemm(out_t.data_ptr(), B, w.desc, ep, ws, stream())
+        torch.cuda.synchronize()
+        return host(res_t), host(xbf, np.uint16), host(pout), host(out_t, np.uint16)
+
+    r_u, x_u, p_u, a_u = run(False)
+    r_f, x_f, p_f, a_f = run(True)
+    assert_bits_equal(r_f, r_u, "residual")
+    assert_bits_equal(x_f, x_u, "xbf")
+    assert_bits_equal(p_f, p_u, "partials_out")
+    if B > 32:  # the merge kernel wrote out on the fused path too
+        assert_bits_equal(a_f, a_u, "out")
+    a = a_u.reshape(B, NQ * HD)
+    r_want, _, _ = orc.qgemm(a, w.w_ref, 2, residual=res0)
+    close(r_u.reshape(B, n), r_want, "o-projection residual vs oracle")
