@@ -31,10 +31,10 @@ struct MergeArgs {
   int target_items;  // the decode launch's plan target: the split count follows from it
 };
 
-// grid (nq, B), one wave each: combine the item partials of (decode row b, q head); the split count
-// follows from the decode plan, recomputed here from the launch's metadata exactly as the decode
-// kernel made it.
-__global__ void __launch_bounds__(64) attn_merge_kernel(MergeArgs a, BatchArgs batch) {
+// grid (nq, B): combine the item partials of (decode row b, q head); the split count follows from
+// the decode plan, recomputed here from the launch's metadata exactly as the decode kernel made it.
+__global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, BatchArgs batch) {
+  __shared__ MergeShared sh;
   const int hq = blockIdx.x, b = blockIdx.y;
   const int L = decode_len(batch, b);
   if (L == 0) return;
@@ -42,8 +42,8 @@ __global__ void __launch_bounds__(64) attn_merge_kernel(MergeArgs a, BatchArgs b
   const DecodePlan pl = wave_decode_plan(batch, a.nkv, a.max_splits, a.target_items);
   const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), pl.cp);
   const float* src = a.scratch + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
-  merge_row_quads(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
-                  a.out + (size_t(row) * a.nq + hq) * kHeadDim);
+  merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
+               a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
 }
 
 constexpr int kBlocksPerCu = 2;
@@ -90,7 +90,8 @@ int launch_attention_merge(const q38a_attention_params& p, const q38a_batch_desc
   if (int rc = decode_grid(&grid, &target)) return rc;
   MergeArgs m{p.gate,          p.ld_gate,       p.out,       p.num_q_heads, p.num_kv_heads,
               p.num_q_heads / p.num_kv_heads, p.split_scratch, p.max_splits, target};
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(64), 0, stream, m, to_args(b));
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.num_q_heads, b.num_seqs), dim3(kMergeThreads), 0, stream, m,
+                     to_args(b));
   return check_hip(hipGetLastError(), "attention merge launch");
 }
 

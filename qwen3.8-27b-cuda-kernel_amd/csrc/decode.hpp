@@ -609,56 +609,117 @@ __device__ inline float wave_sum(float x) {
 
 __device__ inline float sigmoid_gate(uint16_t g) { return fast_sigmoid(bf16_value(g)); }
 
-// Gated merge of one (row, q head)'s split partials for dims d..d+3 (reference
-// attention_decode.cu:241-257): M = max_s m_s, w_s = 2^(m_s - M), a = sum_s w_s acc_s,
-// l = sum_s w_s l_s, y = (a / l) * sigmoid(gate), sums in ascending split order. Split s sits at
-// src + s * stride: acc[256], m, l; m = -inf marks an empty split (weight 0). One thread computes
-// all of it for its four dims, kMergeBatch splits' loads in flight. Not inlined: every caller (the
-// merge kernels, the o-projection's A staging) runs the same instructions, so produces the same bits
-// (inlined, the compiler is free to schedule and contract the arithmetic per call site).
-__device__ __attribute__((noinline)) void merge_quad(const float* src, int splits, int stride, int d, const uint16_t* gate4,
-                                  uint16_t (&y)[4]) {
-  float M = -INFINITY;
-  for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
-    float mv[kMergeBatch];
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) mv[u] = src[size_t(min(s0 + u, splits - 1)) * stride + kHeadDim];
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) M = fmaxf(M, mv[u]);  // (clamped loads repeat the last split)
-  }
-  float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
-    float4_t v[kMergeBatch];
-    float2 ml[kMergeBatch];
+// Gated merge of one (row, q head)'s split partials (reference attention_decode.cu:241-257):
+// M = max_s m_s, a = sum_s 2^(m_s - M) acc_s, l = sum_s 2^(m_s - M) l_s, y = (a / l) * sigmoid(gate).
+// The merge kernels fold the splits in kMergeWaves interleaved running states (state w: splits w,
+// w + kMergeWaves, ...) and combine the states; the o-projection's A staging (qgemm.hip) replays
+// the same steps in one thread. Every multiply-add below is an explicit fmaf, so the result does
+// not depend on the call site's contraction and both produce the same bits.
+
+// Folds the splits s = first, first + step, ... (< splits) of one (row, q head) into a running
+// log-sum-exp state (M, lsum, acc[4] of dims d..d+3), kMergeBatch splits in flight per lane.
+// Split s sits at src + s * stride: acc[256], m, l; m = -inf marks an empty split.
+__device__ inline void fold_splits(const float* src, int first, int step, int splits, size_t stride, int d, float& M,
+                                   float& lsum, float (&acc)[4]) {
+  for (int s0 = first; s0 < splits; s0 += step * kMergeBatch) {
+    float2 v[kMergeBatch][2], ml[kMergeBatch];
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
-      const float* p = src + size_t(min(s0 + u, splits - 1)) * stride;
-      v[u] = *reinterpret_cast<const float4_t*>(p + d);
+      const int s = min(s0 + step * u, splits - 1);
+      const float* p = src + s * stride;
+      v[u][0] = *reinterpret_cast<const float2*>(p + d);
+      v[u][1] = *reinterpret_cast<const float2*>(p + d + 2);
       ml[u] = *reinterpret_cast<const float2*>(p + kHeadDim);
+      if (s0 + step * u >= splits) ml[u].x = -INFINITY;
     }
+    float bm = M;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) bm = fmaxf(bm, ml[u].x);
+    if (bm == -INFINITY) continue;  // uniform: (m, l) are the same in every lane
+    const float c = __builtin_amdgcn_exp2f(M - bm);  // M = -inf gives 0
+    M = bm;
+    lsum *= c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= c;
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
-      if (s0 + u >= splits) break;
-      const float w = __builtin_amdgcn_exp2f(ml[u].x - M);
-      l += w * ml[u].y;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += w * v[u][i];
+      const float w = __builtin_amdgcn_exp2f(ml[u].x - M);  // empty split: 0
+      lsum = __builtin_fmaf(w, ml[u].y, lsum);
+      acc[0] = __builtin_fmaf(w, v[u][0].x, acc[0]);
+      acc[1] = __builtin_fmaf(w, v[u][0].y, acc[1]);
+      acc[2] = __builtin_fmaf(w, v[u][1].x, acc[2]);
+      acc[3] = __builtin_fmaf(w, v[u][1].y, acc[3]);
     }
+  }
+}
+
+// Combines the kMergeWaves states of one dim into the gated bf16 output.
+__device__ inline uint16_t merge_combine(const float (&m)[kMergeWaves], const float (&l)[kMergeWaves],
+                                         const float (&acc)[kMergeWaves], uint16_t gate) {
+  float Mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kMergeWaves; ++w) Mx = fmaxf(Mx, m[w]);
+  float a = 0.f, lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kMergeWaves; ++w) {
+    const float f = __builtin_amdgcn_exp2f(m[w] - Mx);  // empty state: 0
+    a = __builtin_fmaf(f, acc[w], a);
+    lsum = __builtin_fmaf(f, l[w], lsum);
+  }
+  return bf16_bits((a / lsum) * sigmoid_gate(gate));
+}
+
+struct alignas(16) MergeShared {
+  float m[kMergeWaves], l[kMergeWaves];
+  float acc[kMergeWaves][kHeadDim];
+};
+
+// The whole workgroup (kMergeWaves waves) merges one (row, q head): wave w folds splits w, w + 4,
+// ..., the waves' states are combined in LDS, and thread t finishes dim t.
+__device__ inline void merge_row_wg(const float* src, int splits, size_t stride, const uint16_t* gate_row,
+                                    uint16_t* out_row, MergeShared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d = 4 * lane;
+  float M = -INFINITY, lsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+  fold_splits(src, wave, kMergeWaves, splits, stride, d, M, lsum, acc);
+  if (lane == 0) {
+    sh.m[wave] = M;
+    sh.l[wave] = lsum;
+  }
+  *reinterpret_cast<float4_t*>(&sh.acc[wave][d]) = float4_t{acc[0], acc[1], acc[2], acc[3]};
+  __syncthreads();
+  const int t = threadIdx.x;
+  float m[kMergeWaves], l[kMergeWaves], at[kMergeWaves];
+#pragma unroll
+  for (int w = 0; w < kMergeWaves; ++w) {
+    m[w] = sh.m[w];
+    l[w] = sh.l[w];
+    at[w] = sh.acc[w][t];
+  }
+  out_row[t] = merge_combine(m, l, at, gate_row[t]);
+}
+
+// The same merge for dims d..d+3 in one thread (the kMergeWaves folds one after the other).
+__device__ inline void merge_quad(const float* src, int splits, size_t stride, int d, const uint16_t* gate4,
+                                  uint16_t (&y)[4]) {
+  float m[kMergeWaves], l[kMergeWaves], acc[kMergeWaves][4];
+#pragma unroll
+  for (int w = 0; w < kMergeWaves; ++w) {
+    m[w] = -INFINITY;
+    l[w] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[w][i] = 0.f;
+    fold_splits(src, w, kMergeWaves, splits, stride, d, m[w], l[w], acc[w]);
   }
   const uint2 g = *reinterpret_cast<const uint2*>(gate4);
   const uint16_t gv[4] = {uint16_t(g.x), uint16_t(g.x >> 16), uint16_t(g.y), uint16_t(g.y >> 16)};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) y[i] = bf16_bits((acc[i] / l) * sigmoid_gate(gv[i]));
-}
-
-// The first wave of the workgroup merges one (row, q head): lane l owns dims 4l + [0, 4).
-__device__ inline void merge_row_quads(const float* src, int splits, int stride, const uint16_t* gate_row,
-                                       uint16_t* out_row) {
-  if (threadIdx.x >= 64) return;
-  const int d = 4 * int(threadIdx.x);
-  uint16_t y[4];
-  merge_quad(src, splits, stride, d, gate_row + d, y);
-  *reinterpret_cast<uint2*>(out_row + d) = uint2{uint32_t(y[0]) | (uint32_t(y[1]) << 16), uint32_t(y[2]) | (uint32_t(y[3]) << 16)};
+  for (int i = 0; i < 4; ++i) {
+    float at[kMergeWaves];
+#pragma unroll
+    for (int w = 0; w < kMergeWaves; ++w) at[w] = acc[w][i];
+    y[i] = merge_combine(m, l, at, gv[i]);
+  }
 }
 
 // merge_row for prefill partial rows (kPartialRowFloats: O / l in fp16, then m, l): split s weighs

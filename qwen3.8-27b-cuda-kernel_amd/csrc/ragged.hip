@@ -131,6 +131,7 @@ struct RaggedMergeArgs {
 // grid: B * nq decode blocks (a workgroup per decode row and q head), then kPrefillRows / 4 blocks
 // per possible merge task (a wave per row of the split tile).
 __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(RaggedMergeArgs a, BatchArgs batch) {
+  __shared__ MergeShared sh;
   const int B = batch.num_seqs;
   const int blk = blockIdx.x;
   // The attention kernel has finished (same stream): zero the counters it used for the next launch.
@@ -149,8 +150,8 @@ __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(Ragged
     const int row = batch.seq_start[b];
     const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), a.header[0]);
     const float* src = a.decode_partials + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
-    merge_row_quads(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
-                    a.out + (size_t(row) * a.nq + hq) * kHeadDim);
+    merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
+                 a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
     return;
   }
   const int idx = blk - B * a.nq;
