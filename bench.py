@@ -261,18 +261,19 @@ def inproj_config(name, steps, warmup):
 OPROJ_COPIES = 14  # 14 x 20 MB of o-projection weights: more than the 256 MB MALL
 
 
-def oproj_config(name, steps, warmup):
+def oproj_setup(name):
     """The attention layer's tail on a decode step (config 2 contexts for "o_proj_b8", 5a for
     "o_proj_long_b8"): split attention, then the o-projection (W_o 5,120 x 6,144, bq5) with the
-    residual epilogue. Unfused: q38a_attention_decode (split kernel + merge kernel writing out), then
-    q38a_qgemm on out. Fused: q38a_attention_decode_partials, then q38a_qgemm_merge_oproj (the merge
-    inside the GEMM's A staging). Launch i uses KV pool i % 3 and weight copy i % OPROJ_COPIES."""
+    residual epilogue. Returns (unfused(i), fused(i), gemm_only(i), facts). Unfused:
+    q38a_attention_decode (split kernel + merge kernel writing out), then q38a_qgemm on out. Fused:
+    q38a_attention_decode_partials, then q38a_qgemm_merge_oproj (the merge inside the GEMM's A
+    staging). Launch i uses KV pool i % 3 and weight copy i % OPROJ_COPIES."""
     import torch
     import q38a
     from q38a import gemm
     from q38a.workloads import DecodeBatch, decode_contexts
     s = torch.cuda.current_stream().cuda_stream
-    ctx_name = "decode_b8" if name == "o_proj_b8" else "long_b8"
+    ctx_name = "long_b8" if "long" in name else "decode_b8"
     b = DecodeBatch(decode_contexts(ctx_name), seed=0, pools=3)
     gen = torch.Generator(device="cuda").manual_seed(1)
     n, K, B = 5120, 6144, b.B
@@ -299,6 +300,15 @@ def oproj_config(name, steps, warmup):
 
     def gemm_only(i):
         gemm.qgemm(b.out.data_ptr(), B, ws_[i % OPROJ_COPIES][0], ep, ws, s)
+
+    return unfused, fused, gemm_only, {"B": B, "n": n, "k": K, "keep": (b, ws_, res, xbf, pout, wsp, wsc)}
+
+
+def oproj_config(name, steps, warmup):
+    """oproj_setup's three ways, timed with HIP events."""
+    import torch
+    unfused, fused, gemm_only, f = oproj_setup(name)
+    B, n, K = f["B"], f["n"], f["k"]
 
     def timed(fn):
         for i in range(warmup):
@@ -400,6 +410,9 @@ def profile_workload(name, reps=20):
         run = lambda i: q38a.attention_prefill(ap, rb.batch, kvd, s)  # noqa: E731
     elif base in ("in_proj_b8", "in_proj_2048"):
         run, _, _, keep = inproj_setup(base)
+    elif base in ("o_proj_b8", "o_proj_b8_fused"):
+        unfused, fused, _, keep = oproj_setup("o_proj_b8")
+        run = fused if base.endswith("fused") else unfused
     elif base == "mixed":
         rb = RaggedBatch(mixed_seqs(0), dtype=q38a.KV_INT8_VT if vt else q38a.KV_INT8, seed=0, pools=3)
         ap, descs = rb.attention_params(), [rb.kv_desc(i) for i in range(3)]
