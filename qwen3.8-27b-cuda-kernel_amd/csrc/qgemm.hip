@@ -91,6 +91,16 @@ struct BWords {
   uint32_t scale;  // bf16 bits in the low half (converted where used, so the load is not awaited early)
 };
 
+// A wave-uniform address kept in scalar registers (a buffer resource built from an address the
+// compiler computed in vector registers would otherwise be legalised lane by lane).
+template <class T>
+__device__ inline T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(v)));
+  const uint64_t hi = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(v >> 32)));
+  return reinterpret_cast<T*>(lo | (hi << 32));
+}
+
 // Buffer resources over the three weight planes: the per-group offsets are wave-uniform (scalar
 // offsets), the lane's part a fixed vector offset, so no per-load 64-bit address arithmetic.
 struct BPlanes {
@@ -430,7 +440,8 @@ qgemm_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn) {
   // outside its range and load as zero without a memory request
   const int valid_rows = a.m - m0 < kBM ? a.m - m0 : kBM;
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.a) + size_t(m0) * a.k, short(0), valid_rows * a.k * int(sizeof(uint16_t)), 0x00020000);
+      uniform_ptr(const_cast<uint16_t*>(a.a) + size_t(m0) * a.k), short(0), valid_rows * a.k * int(sizeof(uint16_t)),
+      0x00020000);
   const BPlanes bp = make_bplanes<BITS>(a);
   int aoff[MB];
 #pragma unroll
@@ -504,6 +515,235 @@ qgemm_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn) {
     }
   }
   tile_finish<MB, FUSED>(a, ap, batch, kv, sh, C, tile, z, tn, wave, lane);
+}
+
+// ---- large M: 256 x 256 tiles, weights dequantised once per workgroup --------------------------
+// Eight waves (4 x 2) of 64 rows x 128 columns. Per 64-k group the workgroup stages its A rows and
+// dequantises its 256 columns once into LDS, the weights as bf16(code x scale) (the reference's own
+// weight rounding, qgemm.cu), laid out as the MFMA B operand (block, step, lane, 8 k); every wave
+// reads its operands with conflict-free 16-byte reads and the MFMA accumulates across groups
+// directly: no per-group epilogue, no row-sum MFMA. Each thread loads and dequantises its share of
+// the next group while the waves run the current one; one barrier per group. The tile count fills
+// the CUs, so no split-K.
+constexpr int kBigRows = 256;
+constexpr int kBigWaves = 8;
+constexpr int kBigThreads = 64 * kBigWaves;
+constexpr int kBigAStride = 64 + 8;  // bf16 per staged A row (16 B of padding: conflict-free reads)
+
+struct alignas(16) BigShared {
+  uint16_t b[2][8][4][64][8];           // two groups of the tile's weights: [block][step][lane][k]
+  uint16_t a[2][kBigRows][kBigAStride];  // two groups of the tile's A rows
+  float rs[kBigRows];                    // row scales of the folded RMSNorm
+};
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// Two dequantised codes -> packed bf16(code x scale) (RNE): x0, x1 are fp32 128 + u (u the stored
+// code), sneg = -(128 + 2^(b-1)) * scale, exact in fp32, so fma gives (u - 2^(b-1)) * scale
+// exactly before the one rounding to bf16.
+__device__ inline uint32_t scaled_pair(float x0, float x1, float sc, float sneg) {
+  const float2_t f{__builtin_fmaf(x0, sc, sneg), __builtin_fmaf(x1, sc, sneg)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
+// Codes 2P and 2P + 1 of step S of a lane word (k 16 S + 8 kg + 2P + e) as fp32 128 + u.
+template <int BITS, int S, int P>
+__device__ inline void pair_codes(const BWords& b, float& y0, float& y1) {
+  constexpr int q = 4 * S + P;
+  uint32_t x0 = ((b.lo[S] << (16 - 4 * P)) & 0x000F0000u) | 0x43000000u;  // nibble at bit 4P
+  uint32_t x1 = ((b.lo[S] >> (4 * P)) & 0x000F0000u) | 0x43000000u;       // nibble at bit 16 + 4P
+  if constexpr (BITS == 5) {
+    x0 |= shr<q - 20>(b.hi.x) & 0x00100000u;
+    x1 |= shr<q - 4>(b.hi.x) & 0x00100000u;
+  }
+  if constexpr (BITS == 6) {
+    constexpr int r = 2 * (q & 7);
+    const uint32_t h = q < 8 ? b.hi.x : b.hi.y;
+    x0 |= shr<r - 20>(h) & 0x00300000u;
+    x1 |= shr<r - 4>(h) & 0x00300000u;
+  }
+  y0 = __builtin_bit_cast(float, x0);
+  y1 = __builtin_bit_cast(float, x1);
+}
+
+// The 8 codes of step S (k 16 S + 8 kg + i, i < 8) as fp32 128 + u.
+template <int BITS, int S>
+__device__ inline void step_codes(const BWords& b, float (&x)[8]) {
+  pair_codes<BITS, S, 0>(b, x[0], x[1]);
+  pair_codes<BITS, S, 1>(b, x[2], x[3]);
+  pair_codes<BITS, S, 2>(b, x[4], x[5]);
+  pair_codes<BITS, S, 3>(b, x[6], x[7]);
+}
+
+// load_bwords for a lane-dependent block: the block's part of every offset is per lane (a vector
+// offset), the group's part wave-uniform (scalar), so the buffer resource stays uniform.
+template <int BITS>
+__device__ inline void load_bwords_lane(BWords& b, const BPlanes& p, int nb, int g, int G, int l) {
+  constexpr int hb = BITS == 4 ? 0 : BITS == 5 ? 4 : 8;
+  const int unit0 = nb * G;  // this lane's block at group 0
+  b.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(p.lo, (unit0 * 64 + l) * 16, g * 1024, 0));
+  if constexpr (BITS == 5)
+    b.hi = u32x2{__builtin_amdgcn_raw_buffer_load_b32(p.hi, (unit0 * 64 + l) * hb, g * 64 * hb, 0), 0u};
+  else if constexpr (BITS == 6)
+    b.hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(p.hi, (unit0 * 64 + l) * hb, g * 64 * hb, 0));
+  else b.hi = u32x2{0u, 0u};
+  b.scale = __builtin_amdgcn_raw_buffer_load_b16(p.sc, (unit0 * 32 + (l & 31)) * 2, g * 64, 0);
+}
+
+template <int BITS>
+__device__ inline void dequant_to_lds(BigShared& sh, int buf, const BWords& b, int blk, int l) {
+  const float sc = bf16_value(uint16_t(b.scale));
+  const float sneg = -(128.0f + float(1 << (BITS - 1))) * sc;
+  auto step = [&](auto st) {
+    constexpr int S = decltype(st)::value;
+    float x[8];
+    step_codes<BITS, S>(b, x);
+    const u32x4 w{scaled_pair(x[0], x[1], sc, sneg), scaled_pair(x[2], x[3], sc, sneg),
+                  scaled_pair(x[4], x[5], sc, sneg), scaled_pair(x[6], x[7], sc, sneg)};
+    *reinterpret_cast<u32x4*>(&sh.b[buf][blk][S][l][0]) = w;
+  };
+  step(std::integral_constant<int, 0>{});
+  step(std::integral_constant<int, 1>{});
+  step(std::integral_constant<int, 2>{});
+  step(std::integral_constant<int, 3>{});
+}
+
+template <int BITS>
+__global__ void __launch_bounds__(kBigThreads) __attribute__((amdgpu_waves_per_eu(2)))
+qgemm_big_kernel(GemmArgs a) {
+  __shared__ BigShared sh;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, kg = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  // (readfirstlane: wave-uniform values the buffer resources are built from stay in scalar registers)
+  const int tn = __builtin_amdgcn_readfirstlane(blockIdx.x % a.tiles_n);
+  const int m0 = __builtin_amdgcn_readfirstlane((blockIdx.x / a.tiles_n) * kBigRows);
+  const int G = a.k / 64;
+  const BPlanes bp = make_bplanes<BITS>(a);
+
+  // the staging thread's half column of weights: block dblk of the tile, lane word dl
+  const int dcol = threadIdx.x & 255, dblk = dcol >> 5, dl = (dcol & 31) + 32 * (threadIdx.x >> 8);
+  const int dnb = tn * 8 + dblk;
+  // and its four 16-byte chunks of A (rows past M load as zero through the buffer's range)
+  const int valid_rows = __builtin_amdgcn_readfirstlane(a.m - m0 < kBigRows ? a.m - m0 : kBigRows);
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(const_cast<uint16_t*>(a.a) + size_t(m0) * a.k), short(0), valid_rows * a.k * int(sizeof(uint16_t)),
+      0x00020000);
+  auto load_a = [&](u32x4 (&v)[4], int g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = int(threadIdx.x) + i * kBigThreads, r = c >> 3, kc = c & 7;
+      v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, (r * a.k + 8 * kc) * 2, 128 * g, 0));
+    }
+  };
+  auto store_a = [&](const u32x4 (&v)[4], int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = int(threadIdx.x) + i * kBigThreads, r = c >> 3, kc = c & 7;
+      *reinterpret_cast<u32x4*>(&sh.a[buf][r][8 * kc]) = v[i];
+    }
+  };
+
+  float16_t C[2][4];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) C[mb][j] = float16_t{};
+
+  if (threadIdx.x < kBigRows) sh.rs[threadIdx.x] = row_scale(a, m0 + threadIdx.x);
+  {
+    BWords b0;
+    u32x4 a0[4];
+    load_bwords_lane<BITS>(b0, bp, dnb, 0, G, dl);
+    load_a(a0, 0);
+    dequant_to_lds<BITS>(sh, 0, b0, dblk, dl);
+    store_a(a0, 0);
+  }
+  __syncthreads();
+  const int glast = G - 1;
+  for (int g = 0; g < G; ++g) {
+    const int cur = g & 1;
+    // the next group's weights and A rows in flight while this group's MFMAs run
+    const int gn = g + 1 < glast ? g + 1 : glast;
+    BWords bn;
+    u32x4 an[4];
+    load_bwords_lane<BITS>(bn, bp, dnb, gn, G, dl);
+    load_a(an, gn);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8_t ao[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        ao[mb] = *reinterpret_cast<const bf16x8_t*>(&sh.a[cur][64 * wm + 32 * mb + (lane & 31)][16 * s + 8 * kg]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8_t bo = *reinterpret_cast<const bf16x8_t*>(&sh.b[cur][4 * wn + j][s][lane][0]);
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) C[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao[mb], bo, C[mb][j], 0, 0, 0);
+      }
+    }
+    // (past the last group: a copy nobody reads)
+    dequant_to_lds<BITS>(sh, cur ^ 1, bn, dblk, dl);
+    store_a(an, cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: C element e of (mb, j): row 64 wm + 32 mb + 8 (e / 4) + 4 kg + e % 4, column
+  // 256 tn + 128 wn + 32 j + lane % 32
+  auto row_of = [&](int mb, int e) { return m0 + 64 * wm + 32 * mb + 8 * (e >> 2) + 4 * kg + (e & 3); };
+  const int col0 = tn * kTileN + 128 * wn + (lane & 31);
+  if (a.kind == Q38A_EPI_RESIDUAL) {
+    // residual += C; xbf = bf16(residual); the wave's 128 columns are one norm block: sums of
+    // squares over its 4 column blocks, then over the 32 lanes of each half
+    float ss[2][16];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        ss[mb][e] = 0.f;
+        const int row = row_of(mb, e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (row < a.m) {
+            const int col = col0 + 32 * j;
+            float* res = a.residual + size_t(row) * a.n + col;
+            const float x = *res + C[mb][j][e];
+            *res = x;
+            a.xbf[size_t(row) * a.n + col] = bf16_bits(x);
+            ss[mb][e] = __builtin_fmaf(x, x, ss[mb][e]);
+          }
+        }
+      }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float v = ss[mb][e];
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        const int row = row_of(mb, e);
+        if ((lane & 31) == 0 && row < a.m) a.partials_out[size_t(row) * a.norm_blocks + (col0 - (lane & 31)) / 128] = v;
+      }
+    return;
+  }
+  __syncthreads();  // sh.rs
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = row_of(mb, e);
+      if (row >= a.m) continue;
+      const float rs = sh.rs[row - m0];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = col0 + 32 * j;
+        if (col >= a.n_store) continue;
+        const float y = C[mb][j][e] * rs;
+        if (a.kind == Q38A_EPI_STORE_F32) static_cast<float*>(a.out)[size_t(row) * a.ldo + col] = y;
+        else static_cast<uint16_t*>(a.out)[size_t(row) * a.ldo + col] = bf16_bits(y);
+      }
+    }
 }
 
 // ---- small M (<= 32 rows): 32 x 256 tiles, sixteen waves ---------------------------------------
@@ -787,9 +1027,24 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
     if (pl.mb != 1) return set_error(Q38A_ERR_INVALID, "qgemm: the merged A needs the small-M kernel");
     mg = *mi;
   }
+  const int mode = ap ? 1 : mi ? 2 : 0;
+  // large M without the fused append: 256 x 256 tiles with the weights dequantised once per
+  // workgroup, when those tiles fill the CUs
+  const int big_tiles = ((m + kBigRows - 1) / kBigRows) * (w.n / kTileN);
+  if (pl.mb == 2 && mode == 0 && big_tiles >= cus) {
+    g.tiles_n = w.n / kTileN;
+    g.splits = 1;
+    const dim3 bgrid{unsigned(big_tiles)}, bblock{unsigned(kBigThreads)};
+    switch (w.bits) {
+      case 4: hipLaunchKernelGGL((qgemm_big_kernel<4>), bgrid, bblock, 0, stream, g); break;
+      case 5: hipLaunchKernelGGL((qgemm_big_kernel<5>), bgrid, bblock, 0, stream, g); break;
+      case 6: hipLaunchKernelGGL((qgemm_big_kernel<6>), bgrid, bblock, 0, stream, g); break;
+      default: return set_error(Q38A_ERR_UNSUPPORTED, "qgemm: %d-bit weights are not supported", w.bits);
+    }
+    return check_hip(hipGetLastError(), "qgemm launch");
+  }
   const dim3 grid(unsigned(pl.tiles_m * pl.tiles_n * pl.splits)), block(unsigned(threads_of(pl.mb)));
   const bool ev1 = m <= 8;
-  const int mode = ap ? 1 : mi ? 2 : 0;
   switch (w.bits) {
     case 4: launch_bits<4>(pl, ev1, mode, grid, block, stream, g, aa, ba, ka, mg); break;
     case 5: launch_bits<5>(pl, ev1, mode, grid, block, stream, g, aa, ba, ka, mg); break;

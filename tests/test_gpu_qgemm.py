@@ -117,6 +117,56 @@ def test_qgemm_residual(orc, m):
     close(host(pout).reshape(m, n // 128), p_want, "partials_out")
 
 
+@pytest.mark.parametrize("bits", [4, 5, 6])
+@pytest.mark.parametrize("kind", ["bf16", "f32", "residual"])
+def test_qgemm_large_m_tiles(orc, bits, kind):
+    """Large M with enough 256 x 256 tiles to fill the CUs: the kernel that dequantises each weight
+    group once per workgroup into bf16(code x scale). m = 1,000 leaves a partial last row tile; 24
+    rows spread over all tiles are checked against the oracle."""
+    m, n, k = 1000, 16384, 256
+    w = Weight(orc, bits, n, k, seed=40 + bits)
+    rng = np.random.default_rng(41)
+    a = randn_bf16(rng, (m, k))
+    a_t = dev(a)
+    rows = np.linspace(0, m - 1, 24).astype(int)
+    ws, keep = workspace(m, n, k)
+    print(f"qgemm large m: bits={bits} kind={kind} m={m} n={n} k={k}", flush=True)
+    if kind == "residual":
+        res0 = rng.standard_normal((m, n)).astype(np.float32) * 4
+        res_t = dev(res0)
+        xbf = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+        pout = torch.zeros(m * n // 128, dtype=torch.float32, device="cuda")
+        ep = gemm.GemmEpilogue(gemm.EPI_RESIDUAL, None, 0, 0, res_t.data_ptr(), xbf.data_ptr(), pout.data_ptr(), None,
+                               0, 1e-6)
+        gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
+        torch.cuda.synchronize()
+        r_want, x_want, p_want = orc.qgemm(a[rows], w.w_ref, 2, residual=res0[rows])
+        close(host(res_t).reshape(m, n)[rows], r_want, "residual")
+        close(bf16_bits_to_f32(host(xbf, np.uint16).reshape(m, n)[rows]), bf16_bits_to_f32(x_want), "xbf")
+        close(host(pout).reshape(m, n // 128)[rows], p_want, "partials_out")
+    elif kind == "f32":
+        n_store = n - 100
+        out = torch.full((m * n,), float("nan"), dtype=torch.float32, device="cuda")
+        ep = gemm.GemmEpilogue(gemm.EPI_STORE_F32, out.data_ptr(), n, n_store, None, None, None, None, 0, 1e-6)
+        gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
+        torch.cuda.synchronize()
+        got = host(out).reshape(m, n)
+        want = orc.qgemm(a[rows], w.w_ref, 3, n_store=n_store)
+        close(got[rows][:, :n_store], want[:, :n_store], "store f32")
+        assert np.isnan(got[:, n_store:]).all()
+    else:
+        partials = rng.uniform(50.0, 200.0, (m, k // 128)).astype(np.float32)
+        p_t = dev(partials)
+        out = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+        ep = gemm.GemmEpilogue(gemm.EPI_STORE_BF16, out.data_ptr(), n, 0, None, None, None, p_t.data_ptr(), k, 1e-6)
+        for rep in range(2):
+            gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
+            torch.cuda.synchronize()
+            got = bf16_bits_to_f32(host(out, np.uint16)).reshape(m, n)
+            want = bf16_bits_to_f32(orc.qgemm(a[rows], w.w_ref, 0, partials_in=partials[rows], hidden=k))
+            close(got[rows], want, f"bf16 rep {rep}")
+
+
 class InProj:
     """The attention in-projection of one layer at the model's shape: W [q | gate | k | v] (14,336 x
     5,120, bq5), hidden rows a, and a paged cache with prior context for every sequence."""
