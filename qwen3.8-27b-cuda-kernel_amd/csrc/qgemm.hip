@@ -196,7 +196,8 @@ struct alignas(16) GemmShared {
 // then the epilogue. C element e of (row block mb, column block j) in this lane: row
 // 32 mb + 8 (e / 4) + 4 (lane / 32) + e % 4 of the tile, column 32 (kNB wave + j) + lane % 32. Every
 // wave of the column tile calls it (K-part waves have ended); sh.rs holds the tile's row scales.
-template <int MB, bool FUSED>
+// EQ: row quads of the MFMA output that can hold rows < M (the split-K traffic skips the others).
+template <int MB, bool FUSED, int EQ = 4>
 __device__ void tile_finish(const GemmArgs& a, const AppendArgs& ap, const BatchArgs& batch, const KvArgs& kv,
                             GemmShared& sh, float16_t (&C)[MB][nb_of(MB)], int tile, int z, int tn, int wave,
                             int lane) {
@@ -214,7 +215,7 @@ __device__ void tile_finish(const GemmArgs& a, const AppendArgs& ap, const Batch
 #pragma unroll
       for (int j = 0; j < kNB; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
+        for (int e = 0; e < 4 * EQ; ++e) {
           const int r = row_of(mb, e) - m0;
           if (m0 + r < a.m)
             __hip_atomic_store(part + (size_t(z) * kBM + r) * kTileN + 32 * (kNB * wave + j) + (lane & 31), C[mb][j][e],
@@ -235,7 +236,7 @@ __device__ void tile_finish(const GemmArgs& a, const AppendArgs& ap, const Batch
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         part, short(0), int(size_t(a.splits) * kBM * kTileN * sizeof(float)), 0x00020000);
     constexpr int kSc1 = 16;  // cache policy bit sc1
-    constexpr int kZB = MB == 1 ? 4 : 2;
+    constexpr int kZB = MB == 1 ? 16 / EQ : 2;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -243,7 +244,7 @@ __device__ void tile_finish(const GemmArgs& a, const AppendArgs& ap, const Batch
 #pragma unroll
         for (int e = 0; e < 16; ++e) C[mb][j][e] = 0.0f;
     for (int zb = 0; zb < a.splits; zb += kZB) {
-      float V[kZB][MB][kNB][16];
+      float V[kZB][MB][kNB][4 * EQ];
 #pragma unroll
       for (int q = 0; q < kZB; ++q) {
         const int zz = zb + q < a.splits ? zb + q : a.splits - 1;
@@ -253,7 +254,7 @@ __device__ void tile_finish(const GemmArgs& a, const AppendArgs& ap, const Batch
 #pragma unroll
           for (int j = 0; j < kNB; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
+            for (int e = 0; e < 4 * EQ; ++e) {
               const int r = row_of(mb, e) - m0;
               const int off = (r * kTileN + 32 * (kNB * wave + j) + (lane & 31)) * int(sizeof(float));
               V[q][mb][j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, off, zoff, kSc1));
@@ -267,7 +268,7 @@ __device__ void tile_finish(const GemmArgs& a, const AppendArgs& ap, const Batch
 #pragma unroll
           for (int j = 0; j < kNB; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) C[mb][j][e] = use ? C[mb][j][e] + V[q][mb][j][e] : C[mb][j][e];
+            for (int e = 0; e < 4 * EQ; ++e) C[mb][j][e] = use ? C[mb][j][e] + V[q][mb][j][e] : C[mb][j][e];
       }
     }
   }
@@ -911,7 +912,7 @@ qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn mi) 
 #pragma unroll
   for (int e = 0; e < 4 * EV; ++e) C[0][0][e] += sh.kpart[wave][e][lane];
   __syncthreads();  // the union's other uses may overwrite kpart from here on
-  tile_finish<1, FUSED>(a, ap, batch, kv, sh, C, tile, z, tn, wave, lane);
+  tile_finish<1, FUSED, EV>(a, ap, batch, kv, sh, C, tile, z, tn, wave, lane);
 }
 
 // Split-K plan. Small M (qgemv_kernel, one 1024-thread workgroup per CU): slices of at most
