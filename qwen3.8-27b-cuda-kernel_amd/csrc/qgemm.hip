@@ -916,8 +916,8 @@ qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn mi) 
 }
 
 // Split-K plan. Small M (qgemv_kernel, one 1024-thread workgroup per CU): slices of at most
-// kSliceG groups (the staged A), and as many as fill the CUs once without a second round; each of
-// the two K parts keeps a group. Larger M (qgemm_kernel): enough workgroups to stream the weights at
+// kSliceG groups (the staged A), and at most as many as fill the CUs once without a second round;
+// each of the two K parts keeps a group. Larger M (qgemm_kernel): enough workgroups to stream the weights at
 // HBM speed (about two per CU), at least four groups per slice.
 struct GemmPlan {
   int mb, tiles_m, tiles_n, splits;
@@ -932,8 +932,12 @@ GemmPlan plan_gemm(int m, int n, int k, int cus) {
   const int tiles = p.tiles_m * p.tiles_n;
   int s = 1;
   if (p.mb == 1) {
-    const int s_min = (G + kSliceG - 1) / kSliceG, s_fill = cus / tiles;
-    s = s_min > s_fill ? s_min : s_fill;
+    // fill the CUs, but keep about 12 groups per slice at least: a slice's fixed costs (staging,
+    // the split-K tail) cost more than idle CUs below that (measured on the o-projection: 8 slices
+    // of 12 groups 17.6 us, 12 slices of 8 groups 19.0 us)
+    const int s_min = (G + kSliceG - 1) / kSliceG, s_fill = cus / tiles, s_work = G / 12;
+    s = s_fill < s_work ? s_fill : s_work;
+    if (s < s_min) s = s_min;
     if (s > G / kparts_of(1)) s = G / kparts_of(1);
     if (s < s_min) s = s_min;  // (G / 2 >= ceil(G / 20) for every G >= 2)
   } else {
