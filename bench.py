@@ -408,6 +408,11 @@ def profile_workload(name, reps=20):
         ap, kvd = rb.attention_params(), rb.kv_desc(0)
         q38a.qk_norm_rope_append(rb.append_params(), rb.batch, kvd, s)
         run = lambda i: q38a.attention_prefill(ap, rb.batch, kvd, s)  # noqa: E731
+    elif base == "prefill_ragged":
+        rb = RaggedBatch([(6000, 2048)], dtype=q38a.KV_INT8_VT if vt else q38a.KV_INT8, seed=0)
+        ap, kvd = rb.attention_params(), rb.kv_desc(0)
+        q38a.qk_norm_rope_append(rb.append_params(), rb.batch, kvd, s)
+        run = lambda i: q38a.attention_ragged(ap, rb.batch, kvd, s)  # noqa: E731
     elif base in ("in_proj_b8", "in_proj_2048"):
         run, _, _, keep = inproj_setup(base)
     elif base in ("o_proj_b8", "o_proj_b8_fused"):

@@ -54,7 +54,9 @@ struct q38a_runner {
   uint16_t* out = nullptr;
   uint16_t* q16 = nullptr;
   float* rope = nullptr;
-  float* scratch = nullptr;
+  float* scratch = nullptr;   // decode split partials
+  float* rscratch = nullptr;  // ragged launches: counters at the front must stay zero between launches,
+                              // so they do not share the decode launch's partials
   MetaLayout meta;
   uint8_t* meta_dev = nullptr;
   uint8_t* meta_host = nullptr;
@@ -69,7 +71,7 @@ struct q38a_runner {
     if (capture_stream) (void)hipStreamDestroy(capture_stream);
     if (meta_host) (void)hipHostFree(meta_host);
     for (void* p : {static_cast<void*>(meta_dev), static_cast<void*>(proj), static_cast<void*>(out),
-                    static_cast<void*>(q16), static_cast<void*>(rope), static_cast<void*>(scratch)})
+                    static_cast<void*>(q16), static_cast<void*>(rope), static_cast<void*>(scratch), static_cast<void*>(rscratch)})
       if (p) (void)hipFree(p);
     if (kv) q38a_kv_cache_destroy(kv);
   }
@@ -191,7 +193,11 @@ int launch_layers(q38a_runner* r, Kind kind, int row0, const q38a_batch_desc& b,
     // decode row, so the launch is bit-reproducible. A one-token chunk would be a decode row there.
     if (kind == Kind::Decode) rc = q38a_attention_decode(&p, &b, &kvd, s);
     else if (kind == Kind::Prefill && b.num_tokens == 1) rc = q38a_attention_prefill(&p, &b, &kvd, s);
-    else rc = q38a_attention_ragged(&p, &b, &kvd, s);
+    else {
+      q38a_attention_params pr = p;
+      pr.split_scratch = r->rscratch;
+      rc = q38a_attention_ragged(&pr, &b, &kvd, s);
+    }
     if (rc) return rc;
   }
   return Q38A_OK;
@@ -245,9 +251,9 @@ int q38a_runner_create(const q38a_runner_options* opt, q38a_runner** out) {
   const size_t nq = size_t(o.num_q_heads);
   const size_t proj_elems = size_t(o.attn_layers) * size_t(r->rows) * size_t(r->ld);
   const size_t out_elems = size_t(o.attn_layers) * size_t(r->rows) * nq * kHeadDim;
-  const size_t scratch = std::max(q38a_split_scratch_floats(o.max_batch + 1, o.num_q_heads, o.max_splits),
-                                  q38a_ragged_scratch_floats(o.max_batch + 1, r->rows, std::max(o.max_chunk, 2),
-                                                             o.num_q_heads, o.num_kv_heads, o.max_splits));
+  const size_t scratch = q38a_split_scratch_floats(o.max_batch + 1, o.num_q_heads, o.max_splits);
+  const size_t rscratch = q38a_ragged_scratch_floats(o.max_batch + 1, r->rows, std::max(o.max_chunk, 2), o.num_q_heads,
+                                                     o.num_kv_heads, o.max_splits);
   auto dmalloc = [&](void** p, size_t bytes, const char* what) {
     if (!rc) rc = check_hip(hipMalloc(p, bytes), what);
     if (!rc) rc = check_hip(hipMemset(*p, 0, bytes), what);
@@ -256,6 +262,7 @@ int q38a_runner_create(const q38a_runner_options* opt, q38a_runner** out) {
   dmalloc(reinterpret_cast<void**>(&r->out), out_elems * 2, "runner_create: out");
   dmalloc(reinterpret_cast<void**>(&r->q16), size_t(r->rows) * nq * kHeadDim * 2, "runner_create: q16");
   dmalloc(reinterpret_cast<void**>(&r->scratch), scratch * sizeof(float), "runner_create: scratch");
+  dmalloc(reinterpret_cast<void**>(&r->rscratch), rscratch * sizeof(float), "runner_create: ragged scratch");
   dmalloc(reinterpret_cast<void**>(&r->meta_dev), r->meta.bytes, "runner_create: metadata");
   dmalloc(reinterpret_cast<void**>(&r->rope), size_t(o.max_context) * kRotaryDim * sizeof(float), "runner_create: rope");
   if (!rc) rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&r->meta_host), r->meta.bytes, 0), "runner_create: pinned metadata");
