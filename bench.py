@@ -91,6 +91,30 @@ def measured_peaks(reps=10):
     return {"hbm_read_gbs": round(best_read, 1), "mfma_fp16_tflops": round(best_mfma, 1)}
 
 
+def read_ceiling(nbytes, launches=30):
+    """The rate one launch reaches when it reads `nbytes` of contiguous device memory once (the read
+    probe over three rotating buffers, so the 256 MB MALL cannot serve a launch from the previous
+    one; HIP events over `launches` back-to-back launches, as the attention launches are timed). A
+    decode launch reads its KV bytes once: this is its ceiling at the same size, fixed costs of a
+    launch included."""
+    import torch
+    from q38a import probe
+    s = torch.cuda.current_stream().cuda_stream
+    n = (int(nbytes) + 32767) // 32768 * 32768
+    bufs = [torch.ones(n, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    sink = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    for i in range(3):
+        probe.read(bufs[i].data_ptr(), n, sink.data_ptr(), 1024, s)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(launches):
+        probe.read(bufs[i % 3].data_ptr(), n, sink.data_ptr(), 1024, s)
+    b.record()
+    torch.cuda.synchronize()
+    del bufs
+    return n / (a.elapsed_time(b) * 1e-3 / launches) / 1e9
+
+
 def decode_config(name, dtype, steps, warmup, pools=3, ctx_name=None):
     import torch
     import q38a
@@ -727,6 +751,10 @@ def main():
     for r in extra.values():
         if "attn_gbs" in r:
             r["hbm_frac_of_measured"] = round(r["attn_gbs"] / peaks["hbm_read_gbs"], 4)
+            if "kv_bytes" in r and str(r.get("config", "")).startswith("long"):
+                ceil = read_ceiling(r["kv_bytes"])
+                r["same_bytes_read_ceiling_gbs"] = round(ceil, 1)
+                r["frac_of_same_bytes_ceiling"] = round(r["attn_gbs"] / ceil, 4)
         if "attn_tflops" in r:
             r["mfma_frac_of_measured"] = round(r["attn_tflops"] / peaks["mfma_fp16_tflops"], 4)
     busy = read_mfma_busy()
@@ -734,6 +762,7 @@ def main():
         extra["prefill_2048_on_6000"]["mfma_busy_frac"] = busy.get("prefill")
     if busy and "mixed_512_plus_7" in extra:
         extra["mixed_512_plus_7"]["mfma_busy_frac"] = busy.get("mixed")
+    head_ceiling = read_ceiling(head["kv_bytes"])
     batch = head.pop("_batch")
     cpu = None if args.no_cpu else cpu_baseline(batch)
     line = {
@@ -758,7 +787,9 @@ def main():
                      "kernel": "attention_decode (attn_decode_kernel + attn_merge_kernel)",
                      "kernel_ms": round(head["attn_ms"], 5),
                      "measured_peak": peaks["hbm_read_gbs"],
-                     "frac_of_measured": round(head["attn_gbs"] / peaks["hbm_read_gbs"], 4)},
+                     "frac_of_measured": round(head["attn_gbs"] / peaks["hbm_read_gbs"], 4),
+                     "same_bytes_read_ceiling": round(head_ceiling, 1),
+                     "frac_of_same_bytes_ceiling": round(head["attn_gbs"] / head_ceiling, 4)},
         "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "tokens_per_s": round(head["tokens_per_s"], 1),
