@@ -352,16 +352,17 @@ def oproj_config(name, steps, warmup):
             "oproj_gemm_only_ms": round(t_g, 5), "saved_ms": round(t_u - t_f, 5)}
 
 
-def runner_decode_config(steps, warmup, layers=16):
-    """Config 2's decode step across all 16 full-attention layers through the native runner
+def runner_decode_config(steps, warmup, layers=16, ctxs=None, name="decode_b8_16_layers_runner"):
+    """A decode step across all 16 full-attention layers through the native runner
     (include/q38a_runtime.h): one hipGraph per batch bucket (metadata upload + append + decode +
-    merge for every layer, 48 kernels), replayed, against the same step launched eagerly. The KV
-    of 16 layers (3.2 GB) is far larger than the 256 MB MALL."""
+    merge for every layer, 48 kernels), replayed, against the same step launched eagerly. Default:
+    config 2's batch, whose KV over 16 layers (3.2 GB) is far larger than the 256 MB MALL; `ctxs`
+    gives another batch (one short row shows what the graph saves when kernels are short)."""
     import torch
     import q38a
     from q38a.runtime import Runner
     from q38a.workloads import INT8_TOKEN_BYTES, LD, decode_contexts
-    ctxs = decode_contexts("decode_b8")
+    ctxs = list(ctxs) if ctxs is not None else decode_contexts("decode_b8")
     pages = sum((c + 1 + 63) // 64 for c in ctxs)
     gen = torch.Generator(device="cuda").manual_seed(0)
     qn = (1.0 + 0.1 * torch.randn(layers * 256, generator=gen, device="cuda")).float()
@@ -404,10 +405,10 @@ def runner_decode_config(steps, warmup, layers=16):
         out[mode] = a.elapsed_time(e) / steps
     kv = layers * sum(c + 1 for c in ctxs) * INT8_TOKEN_BYTES
     r.close()
-    return {"config": "decode_b8_16_layers_runner", "layers": layers, "graph_ms": round(out["graph"], 5),
+    return {"config": name, "ctxs": ctxs, "layers": layers, "graph_ms": round(out["graph"], 5),
             "eager_ms": round(out["eager"], 5), "kv_bytes": kv,
             "graph_kv_gbs": round(kv / (out["graph"] * 1e-3) / 1e9, 1),
-            "graph_tokens_per_s": round(8 / (out["graph"] * 1e-3), 1)}
+            "graph_tokens_per_s": round(len(ctxs) / (out["graph"] * 1e-3), 1)}
 
 
 def profile_workload(name, reps=20):
@@ -738,6 +739,8 @@ def main():
                                                           max(10, args.steps // 2), 3, dtype=q38a.KV_INT8_VT)
     if not only or "runner" in only:
         extra["decode_b8_16_layers_runner"] = runner_decode_config(max(10, args.steps // 5), 3)
+        extra["decode_b1_short_16_layers_runner"] = runner_decode_config(max(10, args.steps // 5), 3, ctxs=[500],
+                                                                         name="decode_b1_short_16_layers_runner")
     for name in ("in_proj_b8", "in_proj_2048"):
         if not only or name in only:
             extra[name] = inproj_config(name, max(10, args.steps // 5), 3)
