@@ -186,9 +186,10 @@ int q38a_ragged_scratch_init(float* split_scratch, void* stream);
  * split_scratch holds q38a_ragged_scratch_floats(...) floats.
  * No counterpart in the reference (its Engine::step, src/engine.cpp:133-182, runs prefill and
  * decode as separate launches); semantics are those of attention_decode / attention_prefill
- * applied to each sequence. The decode rows' key blocks are handed out dynamically, so their
- * fp32 summation order, and rarely a last bf16 bit, can differ from run to run (decode and
- * prefill launches are bit-reproducible). The launch's work counters (decode item queue and
+ * applied to each sequence. The decode rows' key blocks are handed out dynamically, so the
+ * blocks a wave sums, and the fp16 rounding of its probabilities, can differ from run to run: a
+ * decode row's outputs move by up to ~2^-11 of the V magnitude (inside the parity tolerance);
+ * prefill rows, and the decode and prefill launches, are bit-reproducible. The launch's work counters (decode item queue and
  * block claims) live at the front of split_scratch: launches with separate scratch buffers are
  * independent and may run concurrently on different streams; one scratch buffer serves one
  * launch at a time. */
