@@ -202,10 +202,11 @@ __device__ inline Int8Offsets int8_offsets(const PageLayout& L, int kvh, int n16
 // pg: the page; in0: the block's first token within it (a multiple of 16). K rows, int8 V rows and
 // VT V^T quarters advance by 256 bytes per token, K and int8 V scales by 8, VT V scales by 2.
 template <bool VT>
-__device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, int in0, const Int8Offsets& o) {
-  const uint8_t* rows = pg + kHeadDim * in0;
-  const uint8_t* sc = pg + 8 * in0;
+__device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, int in0, const Int8Offsets& o,
+                                       int live_bytes) {
   if constexpr (VT) {
+    const uint8_t* rows = pg + kHeadDim * in0;
+    const uint8_t* sc = pg + 8 * in0;
 #pragma unroll
     for (int g = 0; g < 4; ++g) d.k[g] = *reinterpret_cast<const u32x4*>(rows + o.k + 64 * g);
     d.ks[0] = *reinterpret_cast<const u32x4*>(sc + o.ks);
@@ -225,21 +226,31 @@ __device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, int in0,
   } else {
     // every load is 16 bytes per lane and non-temporal (the bytes are read once): on this page
     // pattern that streams ~7% faster than ordinary loads with 4-byte V words (a read-pattern probe
-    // of the decode launch's loads, 432 MB per launch: 6.28 vs 5.88 TB/s)
+    // of the decode launch's loads, 432 MB per launch: 6.28 vs 5.88 TB/s). The loads go through a
+    // buffer resource over the page whose size is `live_bytes`: 0 turns every load into one that
+    // returns zeros without touching memory, so a wave's last iteration keeps the loop's single
+    // path without fetching a block again (non-temporal bytes are not kept in the L2, so a repeat
+    // is another HBM read).
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(pg), short(0), live_bytes, 0x00020000);
+    const int srow = kHeadDim * in0, ssc = 8 * in0;
+    constexpr int kNT = 2;  // cache policy: non-temporal
 #pragma unroll
-    for (int g = 0; g < 4; ++g) d.k[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows + o.k + 64 * g));
-    d.ks[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sc + o.ks));
-    d.ks[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sc + o.ks + 16));
+    for (int g = 0; g < 4; ++g)
+      d.k[g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.k + 64 * g, srow, kNT));
+    d.ks[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.ks, ssc, kNT));
+    d.ks[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.ks + 16, ssc, kNT));
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows + o.v + kHeadDim * r));
-      d.v[r][0] = w.x;
-      d.v[r][1] = w.y;
-      d.v[r][2] = w.z;
-      d.v[r][3] = w.w;
+    for (int rr = 0; rr < 4; ++rr) {
+      const u32x4 w =
+          __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.v + kHeadDim * rr, srow, kNT));
+      d.v[rr][0] = w.x;
+      d.v[rr][1] = w.y;
+      d.v[rr][2] = w.z;
+      d.v[rr][3] = w.w;
     }
-    d.vs[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sc + o.vs));
-    d.vs[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sc + o.vs + 16));
+    d.vs[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.vs, ssc, kNT));
+    d.vs[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.vs + 16, ssc, kNT));
   }
 }
 
@@ -344,10 +355,10 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   // the block table is read-only during the launch: through the constant address space its
   // wave-uniform entries become scalar loads, which do not wait behind the vector loads in flight
   const __attribute__((address_space(4))) int* btc = (const __attribute__((address_space(4))) int*)(bt);
-  auto load = [&](Int8Block& d, int idx) {
+  auto load = [&](Int8Block& d, int idx, bool live) {
     const int t0 = src.tb + 16 * idx;
     const uint8_t* pg = layer + size_t(btc[t0 / kPageTokens]) * kv.page_bytes;
-    load_int8_block<VT>(d, pg, t0 % kPageTokens, off);
+    load_int8_block<VT>(d, pg, t0 % kPageTokens, off, live ? int(kv.page_bytes) : 0);
   };
   // one lane claims; the value is read (readfirstlane) only when the next block is chosen
   auto claim = [&]() {
@@ -362,7 +373,7 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   int idx = src.first;
   int pending = dynamic ? claim() : 0;
   Int8Block cur, nxt;
-  load(cur, idx);
+  load(cur, idx, true);
   for (;;) {
     // the empty asm pins the claim's use here: without it the compiler reads the claim right after
     // issuing it, which waits for every load in flight
@@ -371,9 +382,10 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
     const int nidx = dynamic ? src.base + c : idx + src.stride;
     const bool more = nidx < src.nblk;  // uniform
     if (more && dynamic) pending = claim();
-    // unconditional (the last iteration reloads the current block): with a single path the
-    // compiler's wait for the current block does not also cover the next block's loads
-    load(nxt, more ? nidx : idx);
+    // unconditional (on the last iteration, loads of the current block's page that read nothing):
+    // with a single path the compiler's wait for the current block does not also cover the next
+    // block's loads
+    load(nxt, more ? nidx : idx, more);
     compute_block<true, VT>(cur, qf, src.tb + 16 * idx, src.te, m_run, l_run, O, j4);
     if (!more) break;
     cur = nxt;
