@@ -9,7 +9,7 @@ namespace {
 // first and the kv heads of one row tile are dispatched together
 template <int DT>
 __global__ void __launch_bounds__(kPThreads, 2) attn_prefill_kernel(PrefillArgs a, BatchArgs batch, KvArgs kv) {
-  __shared__ KvTile tiles[2];
+  __shared__ KvTileFor<4, DT> tiles[2];
   const int tiles_x = int(gridDim.x) / a.nkv;
   const int tile = tiles_x - 1 - int(blockIdx.x) / a.nkv, kvh = int(blockIdx.x) % a.nkv;
   prefill_unit<DT, DT == Q38A_KV_INT8>(a, batch, kv, tiles, blockIdx.y, kvh, tile, 0, 1, nullptr);
@@ -20,7 +20,7 @@ __global__ void __launch_bounds__(kPThreads, 2) attn_prefill_kernel(PrefillArgs 
 // for them) of the four-wave kernel.
 template <int DT>
 __global__ void __launch_bounds__(2 * kPThreads, 1) attn_prefill8_kernel(PrefillArgs a, BatchArgs batch, KvArgs kv) {
-  __shared__ KvTile tiles[2];
+  __shared__ KvTileFor<8, DT> tiles[2];
   const int tiles_x = int(gridDim.x) / a.nkv;
   const int tile = tiles_x - 1 - int(blockIdx.x) / a.nkv, kvh = int(blockIdx.x) % a.nkv;
   prefill_unit<DT, true, 8>(a, batch, kv, tiles, blockIdx.y, kvh, tile, 0, 1, nullptr);

@@ -43,12 +43,21 @@ constexpr int kRowsPerWave = 32;
 constexpr int kRowsPerTile = kPWaves * kRowsPerWave;  // 128 (token, head) rows per workgroup
 static_assert(2 * kRowsPerTile == kPrefillRows, "ragged prefill units are eight-wave tiles");
 // LDS row strides (halves). K rows are read 16 B per lane by 32 different keys (528 B apart: 16
-// consecutive keys cover all banks once). V rows are read by ds_read_b64_tr_b16, four rows of 32 B
-// per 16 lanes. Both are written 16 B per lane by 32 consecutive keys; for the V rows the stride
-// was chosen by measurement: 624 B (and 576, 608, 672) run the whole kernel ~15% faster than 560,
-// 592, 640 or 656 B, i.e. the dequantising stores are sensitive to the row stride modulo 256.
+// consecutive keys cover all banks once). V rows are read by ds_read_b64_tr_b16: 32 lanes read 64
+// contiguous bytes of each of four consecutive key rows.
+//   * int8 pages in eight-wave workgroups: a tile is written 16 lanes per key row (one contiguous
+//     256-byte run of the row per store instruction, whatever the stride), so the V stride serves
+//     the reads: 576 B (144 dwords = 16 mod 64 banks) puts the four rows' 64-byte runs on disjoint
+//     banks. Against 16 keys per store instruction and 624 B rows: LDS bank-conflict cycles 9% ->
+//     5% of CU cycles, config 3 0.420 -> 0.416 ms (four alternating runs of each build; the ragged
+//     launch's eight-wave units are unchanged). The same staging for bf16 and int8 VT pages was
+//     slower (0.415 -> 0.477 and 0.467 -> 0.489 ms: the bf16 loop then spilled).
+//   * the other tiles write 16 B per lane for 16 consecutive keys per store instruction; their V
+//     stride was chosen by measurement: 624 B (and 576, 608, 672) ran the kernel ~15% faster than
+//     560, 592, 640 or 656 B.
 constexpr int kKStride = kHeadDim + 8;
 constexpr int kVStride = kHeadDim + 56;
+constexpr int kVStrideRuns = kHeadDim + 32;
 // int8 VT pages stage V^T: [dim][key] rows of 32 keys (64 B) padded to 80 B; inside each 16-key
 // half the keys are stored in the order 0-3, 8-11, 4-7, 12-15, so the eight keys a lane feeds to
 // one PV MFMA (16 t + 4 kg + [0, 4) and + 8) are one 16-byte read.
@@ -69,13 +78,18 @@ struct PrefillArgs {
   int attn_layer;
 };
 
-struct alignas(16) KvTile {
+template <int VS>
+struct alignas(16) KvTileS {
   uint16_t k[kKeyTile][kKStride];  // dequantised K, [key][dim]
   union {
-    uint16_t v[kKeyTile][kVStride];    // dequantised V, [key][dim]
+    uint16_t v[kKeyTile][VS];          // dequantised V, [key][dim]
     uint16_t vt[kHeadDim][kVtStride];  // int8 VT pages: dequantised V^T, [dim][key] (keys permuted)
   };
 };
+using KvTile = KvTileS<kVStride>;
+using KvTileRuns = KvTileS<kVStrideRuns>;  // int8 pages, eight-wave workgroups
+template <int W, int DT>
+using KvTileFor = std::conditional_t<W == 8 && DT == Q38A_KV_INT8, KvTileRuns, KvTile>;
 
 // One thread's share of a raw int8 tile in registers: K and V codes of key t % 32, dims
 // 32 (t / 32) + [0, 32), and the two scales (group (t / 32) / 2) it needs.
@@ -150,7 +164,8 @@ __device__ inline void store_tile(KvTile& T, const RawTile& R, int key0, int lim
 }
 
 // Eight-wave workgroups (512 threads): a thread's share of a raw int8 tile is half as large, the
-// K and V codes of key t % 32, dims 16 (t / 32) + [0, 16), and the scales of their 64-dim group.
+// K and V codes of key t / 16, dims 16 (t % 16) + [0, 16), and the scales of their 64-dim group (16
+// lanes read a key's whole 256-byte row and write it to LDS as one contiguous run).
 struct RawTile8 {
   u32x4 k, v;
   uint16_t ks, vs;
@@ -158,7 +173,7 @@ struct RawTile8 {
 
 __device__ inline TileOffsets tile_offsets8(const PageLayout& L, int kvh, int tid) {
   TileOffsets o;
-  const int key = tid & 31, slice = tid >> 5;
+  const int key = tid >> 4, slice = tid & 15;
   o.k = int(L.k_row(kvh, key)) + 16 * slice;
   o.ks = int(L.k_scales(kvh, key)) + 2 * (slice >> 2);
   o.v = int(L.v_row(kvh, key)) + 16 * slice;
@@ -189,8 +204,8 @@ __device__ inline void dequant_store16(uint16_t* dst, const u32x4& w, _Float16 s
   d[1] = u32x4{out[4], out[5], out[6], out[7]};
 }
 
-__device__ inline void store_tile(KvTile& T, const RawTile8& R, int key0, int limit, int tid) {
-  const int key = tid & 31, d0 = 16 * (tid >> 5);
+__device__ inline void store_tile(KvTileRuns& T, const RawTile8& R, int key0, int limit, int tid) {
+  const int key = tid >> 4, d0 = 16 * (tid & 15);
   const bool live = key0 + key < limit;
   dequant_store16(&T.k[key][d0], R.k, live ? __builtin_bit_cast(_Float16, R.ks) : _Float16(0.0f));
   dequant_store16(&T.v[key][d0], R.v, live ? __builtin_bit_cast(_Float16, R.vs) : _Float16(0.0f));
@@ -286,8 +301,8 @@ __device__ inline void store_tile(KvTile& T, const RawTileBf16& R, int key0, int
   bf16_store32(&T.v[key][d0], R.v, live);
 }
 
-// Eight-wave workgroups, int8 VT pages: K as RawTile8 (key t % 32, dims 16 (t / 32) + [0, 16) and
-// its group's scale); V^T of dim t / 2, keys 16 (t % 2) + [0, 16) of the tile (one 16-token quarter:
+// Eight-wave workgroups, int8 VT pages: K codes of key t % 32, dims 16 (t / 32) + [0, 16) and
+// their group's scale; V^T of dim t / 2, keys 16 (t % 2) + [0, 16) of the tile (one 16-token quarter:
 // 16 contiguous bytes), and those keys' scales of the dim's group (group-major: 32 contiguous bytes).
 struct RawTileVt8 {
   u32x4 k;
@@ -352,7 +367,8 @@ __device__ inline void store_tile(KvTile& T, const RawTileVt8& R, int key0, int 
 // Four consecutive keys of one dim from V [key][dim] in LDS: the lanes of each 16-lane group pass
 // the addresses of V[key0 + j / 4][dim0 + 4 (j % 4)] (j = lane % 16) and lane j receives
 // V[key0 + 0..3][dim0 + j].
-__device__ inline half4_t v_keys4(const KvTile& T, int key0, int dim0, int j) {
+template <int VS>
+__device__ inline half4_t v_keys4(const KvTileS<VS>& T, int key0, int dim0, int j) {
   typedef __attribute__((address_space(3))) short4_lds* lds_ptr;
   const uint16_t* src = &T.v[key0 + (j >> 2)][dim0 + 4 * (j & 3)];
   const short4_lds r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(src));
@@ -370,7 +386,7 @@ constexpr int kPartialRowFloats = kHeadDim / 2 + 4;
 // (O / l in fp16, then m, l per row in the exp2 domain; m = -inf and l = 0 for a row without keys).
 template <int DT, bool kLookahead = false, int kWavesWG = kPWaves>
 __device__ __attribute__((always_inline)) inline void prefill_unit(const PrefillArgs& a, const BatchArgs& batch,
-                                                                   const KvArgs& kv, KvTile (&tiles)[2], int b,
+                                                                   const KvArgs& kv, KvTileFor<kWavesWG, DT> (&tiles)[2], int b,
                                                                    int kvh, int tile, int part, int parts,
                                                                    float* partial) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -444,7 +460,7 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
       else load_raw(RT, page_rsrc(page_ptr(j * kKeyTile), kv.page_bytes), in_page * kRowBytes, in_page * 8, toff);
     }
   };
-  auto compute = [&](const KvTile& T, int key0) {
+  auto compute = [&](const KvTileFor<kWavesWG, DT>& T, int key0) {
 
     // S^T = K . Q^T: element 4 blk + r is key key0 + 8 blk + 4 kg + r of this lane's row
     float16_t S = {};

@@ -69,7 +69,7 @@ __global__ void __launch_bounds__(kRaggedThreads, 1)
   static_assert(kRaggedThreads == 2 * kPThreads && kRaggedThreads == kPlanThreads, "one block shape for both kinds");
   __shared__ PlanShared plan;
   __shared__ union alignas(16) Work {
-    KvTile tiles[2];
+    KvTileFor<kRaggedWaves, DT> tiles[2];
     DecodeShared<kRaggedWaves> dec;
   } sh;
   const int B = batch.num_seqs;
