@@ -651,21 +651,26 @@ def cpu_baseline(batch, budget_s=20.0):
     # token; rows are independent). ctypes releases the GIL during the call.
     rows = order[:done_tokens]
     cores = min(len(rows), len(os.sched_getaffinity(0)))
-    if kind == "reference" and cores > 1:
+    if cores > 1:
         from concurrent.futures import ThreadPoolExecutor
-        stores = []
+        jobs, stores = [], []
         for b in rows:
             L = batch.ctxs[b] + 1
             k, v = orc.read_back(pool, batch.dtype, 4, batch.block_table, b, L)
-            st = ref.store(4, L)
-            st.k[...] = k
-            st.v[...] = v
-            stores.append((st, f16_to_f32(q16[b]).ravel(), bf16_to_f32(gate[b]), L - 1))
+            q, g = f16_to_f32(q16[b]).ravel(), bf16_to_f32(gate[b])
+            if kind == "reference":
+                st = ref.store(4, L)
+                st.k[...] = k
+                st.v[...] = v
+                stores.append(st)
+                jobs.append(lambda st=st, q=q, g=g, p=L - 1: st.attention_token(24, q, g, p))
+            else:
+                jobs.append(lambda q=q, g=g, p=L - 1, k=k, v=v: orc.attention_token(q, g, p, k, v, 24, 4))
         t0 = time.perf_counter()
         with ThreadPoolExecutor(cores) as ex:
-            list(ex.map(lambda a: a[0].attention_token(24, a[1], a[2], a[3]), stores))
+            list(ex.map(lambda f: f(), jobs))
         wall = time.perf_counter() - t0
-        for st, *_ in stores:
+        for st in stores:
             st.close()
         out["all_cores"] = {"value": done_bytes / wall / 1e9, "cores": cores, "wall_s": round(wall, 3),
                             "tokens_per_s": done_tokens / wall}
