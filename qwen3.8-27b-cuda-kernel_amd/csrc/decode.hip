@@ -37,9 +37,9 @@ __global__ void __launch_bounds__(kMergeThreads) attn_merge_kernel(MergeArgs a, 
   __shared__ MergeShared sh;
   const int hq = blockIdx.x, b = blockIdx.y;
   const int L = decode_len(batch, b);
-  if (L == 0) return;
   const int row = batch.seq_start[b];
   const DecodePlan pl = wave_decode_plan(batch, a.nkv, a.max_splits, a.target_items);
+  if (L == 0) return;
   const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), pl.cp);
   const float* src = a.scratch + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
   merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,

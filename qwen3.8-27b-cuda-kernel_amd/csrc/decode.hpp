@@ -747,6 +747,8 @@ __device__ inline void merge_row_wg(const float* src, int splits, size_t stride,
                                     uint16_t* out_row, MergeShared& sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int d = 4 * lane;
+  // the gate is read before the partials, so its load is not a second round trip after theirs
+  const uint16_t gate = gate_row[threadIdx.x];
   float M = -INFINITY, lsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
   fold_splits(src, wave, kMergeWaves, splits, stride, d, M, lsum, acc);
   if (lane == 0) {
@@ -763,12 +765,13 @@ __device__ inline void merge_row_wg(const float* src, int splits, size_t stride,
     l[w] = sh.l[w];
     at[w] = sh.acc[w][t];
   }
-  out_row[t] = merge_combine(m, l, at, gate_row[t]);
+  out_row[t] = merge_combine(m, l, at, gate);
 }
 
 // The same merge for dims d..d+3 in one thread (the kMergeWaves folds one after the other).
 __device__ inline void merge_quad(const float* src, int splits, size_t stride, int d, const uint16_t* gate4,
                                   uint16_t (&y)[4]) {
+  const uint2 g = *reinterpret_cast<const uint2*>(gate4);  // before the partials' loads
   float m[kMergeWaves], l[kMergeWaves], acc[kMergeWaves][4];
 #pragma unroll
   for (int w = 0; w < kMergeWaves; ++w) {
@@ -778,7 +781,6 @@ __device__ inline void merge_quad(const float* src, int splits, size_t stride, i
     for (int i = 0; i < 4; ++i) acc[w][i] = 0.f;
     fold_splits(src, w, kMergeWaves, splits, stride, d, m[w], l[w], acc[w]);
   }
-  const uint2 g = *reinterpret_cast<const uint2*>(gate4);
   const uint16_t gv[4] = {uint16_t(g.x), uint16_t(g.x >> 16), uint16_t(g.y), uint16_t(g.y >> 16)};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -795,6 +797,7 @@ template <int kBatch>
 __device__ inline void merge_row_h16_b(const float* src, int splits, size_t stride, const uint16_t* gate_row,
                                        uint16_t* out_row) {
   const int d = 4 * (threadIdx.x & 63);
+  const uint2 g = *reinterpret_cast<const uint2*>(gate_row + d);  // before the partials' loads
   float M = -INFINITY, wsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < splits; s0 += kBatch) {
     uint2 v[kBatch];
@@ -827,7 +830,6 @@ __device__ inline void merge_row_h16_b(const float* src, int splits, size_t stri
       acc[3] += w * float(b[1]);
     }
   }
-  const uint2 g = *reinterpret_cast<const uint2*>(gate_row + d);
   const uint16_t gv[4] = {uint16_t(g.x), uint16_t(g.x >> 16), uint16_t(g.y), uint16_t(g.y >> 16)};
   uint16_t o[4];
 #pragma unroll

@@ -30,8 +30,10 @@ struct PlanShared {
 
 // Keys of decode row b (a sequence with exactly one token in the step): [0, seq_pos0[b] + 1).
 __device__ inline int decode_len(const BatchArgs& b, int s) {
-  const int n = b.seq_start[s + 1] - b.seq_start[s];
-  return n == 1 ? b.seq_pos0[s] + 1 : 0;
+  // the three loads are independent (seq_pos0 is read whatever the row's length), so they are one
+  // round trip to memory rather than two
+  const int s0 = b.seq_start[s], s1 = b.seq_start[s + 1], p = b.seq_pos0[s];
+  return s1 - s0 == 1 ? p + 1 : 0;
 }
 
 __device__ inline int ceil_div_i(int a, int b) { return (a + b - 1) / b; }

@@ -145,10 +145,12 @@ __global__ void __launch_bounds__(kMergeThreads) attn_ragged_merge_kernel(Ragged
   }
   if (blk < B * a.nq) {
     const int b = blk / a.nq, hq = blk % a.nq;
+    // all four loads before the branch: one round trip before the partials
     const int L = decode_len(batch, b);
-    if (L == 0) return;
     const int row = batch.seq_start[b];
-    const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), a.header[0]);
+    const int cp = a.header[0];
+    if (L == 0) return;
+    const int splits = ceil_div_i(ceil_div_i(L, kPageTokens), cp);
     const float* src = a.decode_partials + (size_t(b) * a.nq + hq) * a.max_splits * (kHeadDim + 2);
     merge_row_wg(src, splits, kHeadDim + 2, a.gate + size_t(row) * a.ld_gate + hq * kHeadDim,
                  a.out + (size_t(row) * a.nq + hq) * kHeadDim, sh);
