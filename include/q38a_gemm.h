@@ -86,8 +86,11 @@ int q38a_qgemm(const uint16_t* a, int m, const q38a_bq_weight* w, const q38a_gem
  * weight (nq + nq + 2 nkv heads of 256 rows), ep a STORE_BF16 epilogue whose out is proj. The
  * epilogue stores the gate columns into proj (what attention reads) and runs the fused
  * norm / RoPE / append on the q, k and v tiles straight from LDS: q goes to append->q_out, k and v to
- * the cache; the q, k and v columns of proj are not written. Results are bit-identical to
- * q38a_qgemm followed by q38a_qk_norm_rope_append (append->proj and ld_proj must describe ep->out).
+ * the cache; the q, k and v columns of proj are not written. When m is large enough for the
+ * 256 x 256-tile GEMM to fill the GPU (2,048 rows of the in-projection), the call instead runs that
+ * GEMM into proj (every column) and then the append launch, which is faster there. Either way the
+ * results are bit-identical to q38a_qgemm followed by q38a_qk_norm_rope_append (append->proj and
+ * ld_proj must describe ep->out).
  * No counterpart in the reference (SURVEY: the producer side of the attention path). */
 int q38a_qgemm_qkv_append(const uint16_t* a, int m, const q38a_bq_weight* w, const q38a_gemm_epilogue* ep,
                           const q38a_gemm_workspace* ws, const q38a_qk_norm_rope_params* append,

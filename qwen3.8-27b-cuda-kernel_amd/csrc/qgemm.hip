@@ -36,6 +36,8 @@ namespace q38a {
 
 int decode_grid(int* grid, int* target_items);
 int launch_attention_merge(const q38a_attention_params& p, const q38a_batch_desc& b, hipStream_t stream);
+int launch_qk_norm_rope_append(const q38a_qk_norm_rope_params& p, const q38a_batch_desc& b,
+                               const q38a_kv_cache_desc& kv, hipStream_t stream);
 
 namespace {
 
@@ -1033,10 +1035,14 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
     mg = *mi;
   }
   const int mode = ap ? 1 : mi ? 2 : 0;
-  // large M without the fused append: 256 x 256 tiles with the weights dequantised once per
-  // workgroup, when those tiles fill the CUs
+  // large M: 256 x 256 tiles with the weights dequantised once per workgroup, when those tiles fill
+  // the CUs. With the append requested, that GEMM and then the append launch: at these sizes the
+  // append in the per-group-epilogue kernel's column tiles costs more than the proj round trip
+  // (2,048 rows of the in-projection: 0.686 ms fused against 0.455 ms), and the result is then the
+  // same bits as the two calls made separately.
   const int big_tiles = ((m + kBigRows - 1) / kBigRows) * (w.n / kTileN);
-  if (pl.mb == 2 && mode == 0 && big_tiles >= cus) {
+  if (pl.mb == 2 && mode != 2 && big_tiles >= cus) {
+    if (mode == 1) g.kind = ep.kind;
     g.tiles_n = w.n / kTileN;
     g.splits = 1;
     const dim3 bgrid{unsigned(big_tiles)}, bblock{unsigned(kBigThreads)};
@@ -1046,7 +1052,8 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
       case 6: hipLaunchKernelGGL((qgemm_big_kernel<6>), bgrid, bblock, 0, stream, g); break;
       default: return set_error(Q38A_ERR_UNSUPPORTED, "qgemm: %d-bit weights are not supported", w.bits);
     }
-    return check_hip(hipGetLastError(), "qgemm launch");
+    if (int rc = check_hip(hipGetLastError(), "qgemm launch")) return rc;
+    return mode == 1 ? launch_qk_norm_rope_append(*ap, *b, *kv, stream) : Q38A_OK;
   }
   const dim3 grid(unsigned(pl.tiles_m * pl.tiles_n * pl.splits)), block(unsigned(threads_of(pl.mb)));
   const bool ev1 = m <= 8;

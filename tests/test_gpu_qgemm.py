@@ -211,6 +211,8 @@ class InProj:
 @pytest.mark.parametrize("seqs", [
     pytest.param([(130, 1), (5000, 1), (63, 1), (2000, 1), (64, 1), (700, 1), (1, 1), (9000, 1)], id="decode_b8"),
     pytest.param([(300, 200), (40, 1), (0, 64), (1000, 35)], id="mixed_300"),
+    # large M: the fused call runs the 256 x 256-tile GEMM and then the append launch
+    pytest.param([(3000, 2048)], id="chunk_2048"),
 ])
 def test_in_projection_fused_append_matches_unfused(orc, seqs):
     ip = InProj(orc, seqs, seed=21)
