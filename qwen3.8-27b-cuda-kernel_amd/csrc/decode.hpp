@@ -174,7 +174,7 @@ struct Int8Block {
   u32x4 k[4];         // K codes of token t0 + n16, dims 64g + 16 j4 + [0, 16), g = 0..3
   u32x4 ks[2];        // K scales of tokens t0 + 4 j4 + [0, 4): [token][group] fp16
   uint32_t v[4][4];   // int8: [r][w]: V codes of token t0 + 4 j4 + r, dims 16 n16 + 4 w + [0, 4)
-                      // VT:   [g][i]: V codes of dim 64g + 16 i + n16, tokens t0 + 4 j4 + [0, 4)
+                      // VT:   [g][w]: V codes of dim 64 g + lane, tokens t0 + 4 w + [0, 4)
   u32x4 vs[2];        // V scales of tokens t0 + 4 j4 + [0, 4): [token][group] (int8), [group][token] (VT)
 };
 
@@ -190,7 +190,7 @@ __device__ inline Int8Offsets int8_offsets(const PageLayout& L, int kvh, int n16
   o.k = uint32_t(L.k_row(kvh, n16)) + 16 * j4;
   o.ks = uint32_t(L.k_scales(kvh, 4 * j4));
   if constexpr (VT) {
-    o.v = uint32_t(L.vt_code(kvh, n16, 4 * j4));
+    o.v = uint32_t(L.vt_code(kvh, n16 + 16 * j4, 0));  // dim = lane; + 1,024 B per 64 dims
     o.vs = uint32_t(L.vt_scale(kvh, 0, 4 * j4));
   } else {
     o.v = uint32_t(L.v_row(kvh, 4 * j4)) + 16 * n16;
@@ -205,24 +205,38 @@ template <bool VT>
 __device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, int in0, const Int8Offsets& o,
                                        int live_bytes) {
   if constexpr (VT) {
-    const uint8_t* rows = pg + kHeadDim * in0;
-    const uint8_t* sc = pg + 8 * in0;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) d.k[g] = *reinterpret_cast<const u32x4*>(rows + o.k + 64 * g);
-    d.ks[0] = *reinterpret_cast<const u32x4*>(sc + o.ks);
-    d.ks[1] = *reinterpret_cast<const u32x4*>(sc + o.ks + 16);
-    // one load covers dims 64g + 16i + [0, 16) of the block: 256 contiguous bytes
+    // K and its scales as for int8 pages. V: a block's V^T quarter is 256 dims x 16 tokens, 4 KB
+    // contiguous, so lane l reads the 16 tokens of dims 64 q + l (four 16-byte loads, the wave's
+    // loads 1 KB contiguous each); a 4 x 4 word transpose across the four 16-lane rows (two
+    // permlane32 and two permlane16 swaps per four words) then leaves lane (n16, j4) with tokens
+    // 4 j4 + [0, 4) of dims 64 q + 16 i + n16, the layout the PV MFMAs take.
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(pg), short(0), live_bytes, 0x00020000);
+    const int srow = kHeadDim * in0, ssc = 8 * in0;  // 16 tokens further = 4,096 B, for K and V^T
+    constexpr int kNT = 2;  // cache policy: non-temporal
 #pragma unroll
     for (int g = 0; g < 4; ++g)
+      d.k[g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.k + 64 * g, srow, kNT));
+    d.ks[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.ks, ssc, kNT));
+    d.ks[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.ks + 16, ssc, kNT));
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        d.v[g][i] = *reinterpret_cast<const uint32_t*>(rows + o.v + 16 * (64 * g + 16 * i));
-    const uint8_t* vsc = pg + 2 * in0 + o.vs;  // group g at + 128 g: 4 tokens = 8 bytes
-    uint2 s[4];
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o.v + 1024 * q, srow, kNT));
+      d.v[q][0] = w.x;
+      d.v[q][1] = w.y;
+      d.v[q][2] = w.z;
+      d.v[q][3] = w.w;
+    }
+    // V scales, group-major: group g's 4 tokens are 8 contiguous bytes, groups 128 B apart
+    uint32_t sv[4][2];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) s[g] = *reinterpret_cast<const uint2*>(vsc + 2 * kPageTokens * g);
-    d.vs[0] = u32x4{s[0].x, s[0].y, s[1].x, s[1].y};
-    d.vs[1] = u32x4{s[2].x, s[2].y, s[3].x, s[3].y};
+    for (int g = 0; g < 4; ++g) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, o.vs + 2 * kPageTokens * g, 2 * in0, kNT);
+      sv[g][0] = x[0];
+      sv[g][1] = x[1];
+    }
+    d.vs[0] = u32x4{sv[0][0], sv[0][1], sv[1][0], sv[1][1]};
+    d.vs[1] = u32x4{sv[2][0], sv[2][1], sv[3][0], sv[3][1]};
   } else {
     // every load is 16 bytes per lane and non-temporal (the bytes are read once): on this page
     // pattern that streams ~7% faster than ordinary loads with 4-byte V words (a read-pattern probe
@@ -254,6 +268,25 @@ __device__ inline void load_int8_block(Int8Block& d, const uint8_t* pg, int in0,
   }
 }
 
+// 4 x 4 transpose of 32-bit words across the four 16-lane rows of a wave: afterwards register i
+// of a lane in row j holds what register j held in the lane of row i with the same position in
+// its row (two permlane32 swaps exchange the rows 0-1 / 2-3 halves, two permlane16 swaps the odd
+// and even rows).
+__device__ inline void row_transpose4(uint32_t& a0, uint32_t& a1, uint32_t& a2, uint32_t& a3) {
+  auto r = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
+  a0 = r[0];
+  a2 = r[1];
+  r = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+  a1 = r[0];
+  a3 = r[1];
+  r = __builtin_amdgcn_permlane16_swap(a0, a1, false, false);
+  a0 = r[0];
+  a1 = r[1];
+  r = __builtin_amdgcn_permlane16_swap(a2, a3, false, false);
+  a2 = r[0];
+  a3 = r[1];
+}
+
 // One 16-token block of int8 pages for this lane: S^T = K . Q^T per 64-dim group on fp16 MFMAs
 // (codes exact in fp16, q as stored), the group's K scale applied to the fp32 partial; then
 // O += P' V with P' = p * v_scale per group rounded once to fp16 (relative error <= 2^-11; V codes
@@ -278,7 +311,19 @@ __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][
   float p[4];
   softmax_step(S, valid, m_run, l_run, p, O, j4);
   if constexpr (VT) {
-    // O += P' V, P' = p * v_scale per group rounded once to fp16, V codes exact
+    // O += P' V, P' = p * v_scale per group rounded once to fp16, V codes exact. The block holds
+    // lane l's dims 64 g + l (16 tokens each); the transpose gives lane (n16, j4) tokens
+    // 4 j4 + [0, 4) of dims 64 g + 16 i + n16 in v[g][i].
+    uint32_t v[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t a0 = d.v[g][0], a1 = d.v[g][1], a2 = d.v[g][2], a3 = d.v[g][3];
+      row_transpose4(a0, a1, a2, a3);
+      v[g][0] = a0;
+      v[g][1] = a1;
+      v[g][2] = a2;
+      v[g][3] = a3;
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       half4_t pa;
@@ -287,7 +332,7 @@ __device__ inline void compute_block(const Int8Block& d, const half8_t (&qf)[4][
 #pragma unroll
       for (int i = 0; i < 4; ++i) {  // the word already holds tokens 0..3 of the lane's dim
         half2_t lo, hi;
-        codes4_to_half(d.v[g][i], lo, hi);
+        codes4_to_half(v[g][i], lo, hi);
         O[4 * g + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, half4_t{lo[0], lo[1], hi[0], hi[1]}, O[4 * g + i], 0, 0,
                                                             0);
       }
