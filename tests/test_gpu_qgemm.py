@@ -4,10 +4,14 @@ reference's file layout and repacked by the library (reference src/kernels/qgemm
 the in-projection with the fused norm / RoPE / append, which must equal q38a_qgemm followed by
 q38a_qk_norm_rope_append bit for bit (q, K/V bytes and scales, the gate columns of proj).
 
-GEMM outputs are compared with the oracle's double-precision product over the reference's
-bf16(code * scale) weights within |d| <= 1e-2 |ref| + 1e-2 rms(ref): the kernel accumulates in fp32
-and applies each group's scale to the exact code sum instead of rounding every weight to bf16
-first, so it differs from the reference by about one bf16 rounding of the output."""
+The oracle's double-precision product is taken over the weights the kernel path multiplies by:
+  * the 256 x 256-tile kernel (large M) dequantises each weight to bf16(code x scale), the
+    reference's own weight rounding, so it is checked against those weights;
+  * the other kernels apply each group's scale in fp32 to the exact code sum, so they are checked
+    against the exact weights code x scale (exact in fp32).
+The bound is one output rounding step plus the fp32 accumulation: |d| <= ulp(ref) + 2^-18 (|A| |W'|^T)
+x rs, where ulp is the bf16 (or fp32) spacing at |ref| and W' bounds the magnitude the kernel sums
+(|W| for bf16 weights; 256 x scale for the offset codes 128 + u of the exact path)."""
 import numpy as np
 import pytest
 import torch
@@ -21,16 +25,43 @@ from util import assert_bits_equal, bf16_bits_to_f32, f32_to_bf16_bits, randn_bf
 pytestmark = pytest.mark.gpu
 
 
-def close(got, want, what):
+def bf16_ulp(x):
+    """Spacing of bf16 at |x| (2^(e - 7) for |x| in [2^e, 2^(e + 1)); the smallest normal's below)."""
+    e = np.floor(np.log2(np.maximum(np.abs(np.asarray(x, np.float64)), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def close(got, want, what, a=None, wmag=None, rs=None, out="bf16"):
+    """|got - want| <= ulp(want) + 2^-18 (|A| wmag^T) rs (see the module docstring); `out` names the
+    stored type whose rounding step is allowed ("bf16" or "f32")."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
-    rms = float(np.sqrt(np.mean(want ** 2))) if want.size else 0.0
     d = np.abs(got - want)
-    bound = 1e-2 * np.abs(want) + 1e-2 * rms
+    ulp = bf16_ulp(want) if out == "bf16" else np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    acc = 0.0
+    if a is not None:
+        acc = 2.0 ** -18 * (np.abs(bf16_bits_to_f32(a).astype(np.float64)) @ np.asarray(wmag, np.float64).T)
+        if rs is not None:
+            acc = acc * np.asarray(rs, np.float64)[:, None]
+    bound = ulp + acc
     assert np.isfinite(got).all(), f"{what}: non-finite"
     bad = d > bound
-    assert not bad.any(), f"{what}: {int(bad.sum())} of {d.size} outside; worst {float((d - bound).max()):.3g} (rms {rms:.3g})"
-    print(f"{what}: max |d| {float(d.max()):.3g}, rms(ref) {rms:.3g}", flush=True)
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {d.size} outside one rounding step + accumulation; "
+                           f"worst excess {float((d - bound).max()):.3g}")
+    print(f"{what}: max |d| / bound {float((d / bound).max()):.3f}, max |d| / ulp {float((d / ulp).max()):.3f}",
+          flush=True)
+
+
+def row_scales(partials, hidden, eps=1e-6):
+    p = np.asarray(partials, np.float32)
+    return 1.0 / np.sqrt(p.sum(1, dtype=np.float64) / hidden + eps)
+
+
+def big_path(m, n):
+    """Whether q38a_qgemm takes the 256 x 256-tile kernel (bf16 weights) for m rows of n columns: its
+    planner picks it when there are more than 32 rows and the tiles fill the CUs."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return m > 32 and ((m + 255) // 256) * (n // 256) >= cus
 
 
 class Weight:
@@ -43,11 +74,36 @@ class Weight:
         codes = rng.integers(-(1 << (bits - 1)), 1 << (bits - 1), (n, k)).astype(np.int8)
         scales = f32_to_bf16_bits(rng.uniform(scale_lo, scale_hi, (n, k // 64)).astype(np.float32))
         lo, hi, sc = orc.bq_pack_file(bits, codes, scales)
-        self.w_ref = orc.bq_file_weight(bits, n, k, lo, hi, sc)
+        self.w_ref = orc.bq_file_weight(bits, n, k, lo, hi, sc)  # bf16(code x scale), the reference's
+        scale_f32 = np.repeat(bf16_bits_to_f32(scales), 64, 1)
+        self.w_exact = codes.astype(np.float32) * scale_f32  # exact in fp32 (<= 6 + 8 significant bits)
+        self.w_offset_mag = 256.0 * scale_f32
         rlo, rhi, rsc = gemm.repack(bits, n, k, lo, hi, sc)
         self.t = [dev(rlo), dev(rhi) if rhi is not None else None, dev(rsc)]
         self.desc = gemm.BQWeight(self.t[0].data_ptr(), self.t[1].data_ptr() if self.t[1] is not None else None,
                                   self.t[2].data_ptr(), bits, n, k, n)
+
+
+def oracle_weight(w, m):
+    """(weights the kernel path for m rows multiplies by, the magnitude bound its fp32 sums carry)"""
+    return (w.w_ref, np.abs(w.w_ref)) if big_path(m, w.n) else (w.w_exact, w.w_offset_mag)
+
+
+def check_residual(orc, w, a, res0, res, xbf, pout, m=None):
+    """The Residual epilogue against the oracle: residual within one fp32 step + accumulation, its
+    bf16 copy within one bf16 step + accumulation, each 128-column sum of squares within the bound
+    those residual errors imply (2 sum |r| e + one fp32 step)."""
+    n = w.n
+    wo, wmag = oracle_weight(w, m if m is not None else a.shape[0])
+    r_want, x_want, p_want = orc.qgemm(a, wo, 2, residual=res0)
+    close(res, r_want, "residual", a, wmag, out="f32")
+    close(bf16_bits_to_f32(xbf), bf16_bits_to_f32(x_want), "xbf", a, wmag)
+    acc = 2.0 ** -18 * (np.abs(bf16_bits_to_f32(a).astype(np.float64)) @ wmag.T.astype(np.float64))
+    e = acc + np.spacing(np.abs(r_want)).astype(np.float64)
+    pb = (2 * np.abs(r_want.astype(np.float64)) * e).reshape(len(r_want), n // 128, 128).sum(-1)
+    pb += np.spacing(np.abs(p_want)).astype(np.float64) * 4
+    d = np.abs(pout.astype(np.float64) - p_want)
+    assert (d <= pb).all(), f"partials_out: {int((d > pb).sum())} outside; worst excess {float((d - pb).max()):.3g}"
 
 
 def workspace(m, n, k):
@@ -74,8 +130,9 @@ def test_qgemm_store_bf16_folded_norm(orc, bits, m):
         gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
         torch.cuda.synchronize()
         got = bf16_bits_to_f32(host(out, np.uint16)).reshape(m, n)
-        want = bf16_bits_to_f32(orc.qgemm(a, w.w_ref, 0, partials_in=partials, hidden=k))
-        close(got, want, f"bits {bits} m {m} rep {rep}")
+        wo, wmag = oracle_weight(w, m)
+        want = bf16_bits_to_f32(orc.qgemm(a, wo, 0, partials_in=partials, hidden=k))
+        close(got, want, f"bits {bits} m {m} rep {rep}", a, wmag, row_scales(partials, k))
 
 
 def test_qgemm_store_f32_and_partial_columns(orc):
@@ -90,8 +147,9 @@ def test_qgemm_store_f32_and_partial_columns(orc):
     gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
     torch.cuda.synchronize()
     got = host(out).reshape(m, n)
-    want = orc.qgemm(a, w.w_ref, 3, n_store=n_store)
-    close(got[:, :n_store], want[:, :n_store], "store f32")
+    wo, wmag = oracle_weight(w, m)
+    want = orc.qgemm(a, wo, 3, n_store=n_store)
+    close(got[:, :n_store], want[:, :n_store], "store f32", a, wmag[:n_store], out="f32")
     assert np.isnan(got[:, n_store:]).all()  # columns past n_store untouched
 
 
@@ -111,10 +169,8 @@ def test_qgemm_residual(orc, m):
                            1e-6)
     gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
     torch.cuda.synchronize()
-    r_want, x_want, p_want = orc.qgemm(a, w.w_ref, 2, residual=res0)
-    close(host(res_t).reshape(m, n), r_want, "residual")
-    close(bf16_bits_to_f32(host(xbf, np.uint16)).reshape(m, n), bf16_bits_to_f32(x_want), "xbf")
-    close(host(pout).reshape(m, n // 128), p_want, "partials_out")
+    check_residual(orc, w, a, res0, host(res_t).reshape(m, n), host(xbf, np.uint16).reshape(m, n),
+                   host(pout).reshape(m, n // 128))
 
 
 @pytest.mark.parametrize("bits", [4, 5, 6])
@@ -140,10 +196,8 @@ def test_qgemm_large_m_tiles(orc, bits, kind):
                                0, 1e-6)
         gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
         torch.cuda.synchronize()
-        r_want, x_want, p_want = orc.qgemm(a[rows], w.w_ref, 2, residual=res0[rows])
-        close(host(res_t).reshape(m, n)[rows], r_want, "residual")
-        close(bf16_bits_to_f32(host(xbf, np.uint16).reshape(m, n)[rows]), bf16_bits_to_f32(x_want), "xbf")
-        close(host(pout).reshape(m, n // 128)[rows], p_want, "partials_out")
+        check_residual(orc, w, a[rows], res0[rows], host(res_t).reshape(m, n)[rows],
+                       host(xbf, np.uint16).reshape(m, n)[rows], host(pout).reshape(m, n // 128)[rows], m=m)
     elif kind == "f32":
         n_store = n - 100
         out = torch.full((m * n,), float("nan"), dtype=torch.float32, device="cuda")
@@ -151,8 +205,9 @@ def test_qgemm_large_m_tiles(orc, bits, kind):
         gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
         torch.cuda.synchronize()
         got = host(out).reshape(m, n)
-        want = orc.qgemm(a[rows], w.w_ref, 3, n_store=n_store)
-        close(got[rows][:, :n_store], want[:, :n_store], "store f32")
+        wo, wmag = oracle_weight(w, m)
+        want = orc.qgemm(a[rows], wo, 3, n_store=n_store)
+        close(got[rows][:, :n_store], want[:, :n_store], "store f32", a[rows], wmag[:n_store], out="f32")
         assert np.isnan(got[:, n_store:]).all()
     else:
         partials = rng.uniform(50.0, 200.0, (m, k // 128)).astype(np.float32)
@@ -163,8 +218,9 @@ def test_qgemm_large_m_tiles(orc, bits, kind):
             gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
             torch.cuda.synchronize()
             got = bf16_bits_to_f32(host(out, np.uint16)).reshape(m, n)
-            want = bf16_bits_to_f32(orc.qgemm(a[rows], w.w_ref, 0, partials_in=partials[rows], hidden=k))
-            close(got[rows], want, f"bf16 rep {rep}")
+            wo, wmag = oracle_weight(w, m)
+            want = bf16_bits_to_f32(orc.qgemm(a[rows], wo, 0, partials_in=partials[rows], hidden=k))
+            close(got[rows], want, f"bf16 rep {rep}", a[rows], wmag, row_scales(partials[rows], k))
 
 
 class InProj:
@@ -224,8 +280,10 @@ def test_in_projection_fused_append_matches_unfused(orc, seqs):
     assert_bits_equal(proj_f[:, gate], proj_u[:, gate], "gate columns of proj")
     # the unfused projection against the oracle (every row for small m, 24 rows otherwise)
     rows = np.arange(ip.m) if ip.m <= 16 else np.linspace(0, ip.m - 1, 24).astype(int)
-    want = orc.qgemm(ip.a[rows], ip.w.w_ref, 0, partials_in=ip.partials[rows], hidden=ip.k)
-    close(bf16_bits_to_f32(proj_u[rows]), bf16_bits_to_f32(want), "in-projection vs oracle")
+    wo, wmag = oracle_weight(ip.w, ip.m)
+    want = orc.qgemm(ip.a[rows], wo, 0, partials_in=ip.partials[rows], hidden=ip.k)
+    close(bf16_bits_to_f32(proj_u[rows]), bf16_bits_to_f32(want), "in-projection vs oracle", ip.a[rows], wmag,
+          row_scales(ip.partials[rows], ip.k))
 
 
 @pytest.mark.parametrize("ctxs,n", [
@@ -284,5 +342,4 @@ def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n):
     if B > 32:  # the merge kernel wrote out on the fused path too
         assert_bits_equal(a_f, a_u, "out")
     a = a_u.reshape(B, NQ * HD)
-    r_want, _, _ = orc.qgemm(a, w.w_ref, 2, residual=res0)
-    close(r_u.reshape(B, n), r_want, "o-projection residual vs oracle")
+    check_residual(orc, w, a, res0, r_u.reshape(B, n), x_u.reshape(B, n), p_u.reshape(B, n // 128))
