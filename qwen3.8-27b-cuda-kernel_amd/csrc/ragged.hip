@@ -66,10 +66,13 @@ __device__ inline int parts_of(const BatchArgs& batch, int s, int chunk) {
 template <int DT>
 __global__ void __launch_bounds__(kRaggedThreads, 1)
     attn_ragged_kernel(RaggedArgs r, DecodeArgs d, PrefillArgs pa, BatchArgs batch, KvArgs kv) {
-  static_assert(kRaggedThreads == 2 * kPThreads && kRaggedThreads == kPlanThreads, "one block shape for both kinds");
+  static_assert(kRaggedThreads == kPThreads && kRaggedThreads == kPlanThreads, "one block shape for both kinds");
   __shared__ PlanShared plan;
   __shared__ union alignas(16) Work {
-    KvTileFor<kRaggedWaves, DT> tiles[2];
+    struct {
+      KvTileFor<DT> tiles[2];
+      std::conditional_t<kQHalfInLds<DT>, QHalfLds, char> qh;
+    } pre;
     DecodeShared<kRaggedWaves> dec;
   } sh;
   const int B = batch.num_seqs;
@@ -100,9 +103,12 @@ __global__ void __launch_bounds__(kRaggedThreads, 1)
       const int parts = parts_of(batch, b, chunk);
       const int tile_r = local / (pa.nkv * parts), rem = local % (pa.nkv * parts);
       const int tile = prefill_tiles(n, pa.group) - 1 - tile_r;
-      prefill_unit<DT, DT != Q38A_KV_BF16, kRaggedWaves>(pa, batch, kv, sh.tiles, b, rem / parts, tile, rem % parts,
+      QHalfLds* qp = nullptr;
+      if constexpr (kQHalfInLds<DT>) qp = &sh.pre.qh;
+      prefill_unit<DT>(pa, batch, kv, sh.pre.tiles, b, rem / parts, tile, rem % parts,
                                                          parts,
-                                                         r.prefill_partials + size_t(u) * kPrefillRows * kPartialRowFloats);
+                                                         r.prefill_partials + size_t(u) * kPrefillRows * kPartialRowFloats,
+                                                         qp);
     }
   } else {
     const DecodePlan pl = wave_decode_plan(batch, d.nkv, d.max_splits, d.target_items);

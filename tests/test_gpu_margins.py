@@ -6,7 +6,8 @@ data's own scale; otherwise a 2^-10 output would pass any absolute bound. Both l
 printed for every case.
 
 What these probe: decode rounds P' = p * v_scale to fp16, which is subnormal for small V groups;
-prefill stages dequantised K/V tiles as fp16 (bf16 pages: exact only within fp16's normal range);
+prefill feeds the exact K codes to the MFMA and applies the K scale to the fp32 group partials (V is
+staged dequantised as fp16; bf16 pages: exact only within fp16's normal range);
 large K makes the softmax nearly one-hot, so the running-max rescaling is exercised at every block.
 """
 import numpy as np
@@ -25,10 +26,6 @@ SCALES = [
     pytest.param((2.0 ** 10, 2.0 ** -10, None), id="large_k_small_v"),
     pytest.param((1.0, 1.0, (37, 64.0)), id="dominant_key"),
 ]
-# The int8 prefill path rounds each dequantised K value to fp16 (as the reference's fp16 staging
-# does), so its scores are exact only to ~2^-12 relative: with K ~ 2^10 the softmax is nearly one-hot
-# and near-ties between the top two keys (a fraction of a percent of (row, head) pairs) can flip.
-PREFILL_K_STAGED_FP16 = True
 DTYPES = [pytest.param(q38a.KV_INT8, id="int8"), pytest.param(q38a.KV_BF16, id="bf16"),
           pytest.param(q38a.KV_INT8_VT, id="int8_vt")]
 
@@ -51,14 +48,27 @@ def test_decode_margins(orc, kv_dtype, case):
 
 @pytest.mark.parametrize("kv_dtype", DTYPES)
 @pytest.mark.parametrize("case", SCALES)
-def test_ragged_margins(orc, kv_dtype, case, request):
+def test_ragged_margins(orc, kv_dtype, case):
     """A split prefill chunk, an unsplit one and decode rows in one ragged launch."""
     k_scale, v_scale, dominant = case
-    if kv_dtype != q38a.KV_BF16 and (k_scale > 1.0 or dominant) and PREFILL_K_STAGED_FP16:
-        request.applymarker(pytest.mark.xfail(reason="int8 prefill stages K as fp16(code * scale): scores carry a "
-                                                     "2^-12 relative error, which flips near-ties when K ~ 2^10",
-                                              strict=False))
     seqs = [(4000, 40), (9000, 1), (0, 100), (700, 1), (63, 1)]
     got, want = ragged_step(orc, seqs, seed=72, kv_dtype=kv_dtype, k_scale=k_scale, v_scale=v_scale,
                             dominant=dominant, return_out=True)
     report(f"ragged k{k_scale:g} v{v_scale:g} dom={dominant} dtype={kv_dtype}", got, want, v_scale)
+
+
+@pytest.mark.parametrize("kv_dtype", DTYPES)
+@pytest.mark.parametrize("case", SCALES)
+@pytest.mark.parametrize("shape", ["four_wave", "eight_wave"])
+def test_prefill_margins(orc, kv_dtype, case, shape):
+    """The prefill launch in both workgroup shapes: 140 tokens (128-row workgroups, one per CU) and
+    a 1,400-token chunk (256-row workgroups; 14 tokens spread over it are checked)."""
+    from test_gpu_prefill import prefill_step
+    k_scale, v_scale, dominant = case
+    if shape == "four_wave":
+        seqs, checks = [(4000, 40), (0, 100)], None
+    else:
+        seqs, checks = [(3000, 1400)], [[0, 1, 63, 64, 200, 511, 512, 700, 901, 1100, 1300, 1397, 1398, 1399]]
+    got, want = prefill_step(orc, seqs, seed=73, kv_dtype=kv_dtype, check_tokens=checks, k_scale=k_scale,
+                             v_scale=v_scale, dominant=dominant, return_out=True)
+    report(f"prefill {shape} k{k_scale:g} v{v_scale:g} dom={dominant} dtype={kv_dtype}", got, want, v_scale)

@@ -11,21 +11,26 @@ import torch
 import q38a
 from gpu_util import HD, LD, NKV, NQ, Batch, Pool, append_params, attention_params, dev, host, paged_layout, rope_dev, stream
 from util import assert_bits_equal, bf16_bits_to_f32, check_close, randn_bf16
-from test_gpu_decode import build_context
+from test_gpu_decode import build_context, scale_proj_kv
 
 pytestmark = pytest.mark.gpu
 
 
-def prefill_step(orc, seqs, seed, kv_dtype=q38a.KV_INT8, check_tokens=None):
+def prefill_step(orc, seqs, seed, kv_dtype=q38a.KV_INT8, check_tokens=None, k_scale=1.0, v_scale=1.0, dominant=None,
+                 return_out=False):
     """seqs: [(prefix, n)] one chunk per sequence, appended then attended in one prefill launch.
-    check_tokens: per sequence, the chunk-token indices compared with the oracle (default all)."""
+    check_tokens: per sequence, the chunk-token indices compared with the oracle (default all).
+    k_scale, v_scale, dominant: K/V magnitudes of the context and the chunk (see build_context)."""
     rng = np.random.default_rng(seed)
     B = len(seqs)
     bt, pages = paged_layout(rng, [p + n for p, n in seqs])
-    pool_host = build_context(orc, rng, [p for p, _ in seqs], kv_dtype, bt, pages)
+    pool_host = build_context(orc, rng, [p for p, _ in seqs], kv_dtype, bt, pages, k_scale=k_scale, v_scale=v_scale,
+                              dominant=dominant)
     pool = Pool(kv_dtype, pages, bt, fill=pool_host)
     b = Batch([(i, p, n) for i, (p, n) in enumerate(seqs)])
     proj = randn_bf16(rng, (b.M, LD))
+    if k_scale != 1.0 or v_scale != 1.0:
+        proj = scale_proj_kv(rng, proj, k_scale, v_scale)
     q_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
     k_norm = rng.normal(1.0, 0.1, HD).astype(np.float32)
     proj_t, qn_t, kn_t = dev(proj), dev(q_norm), dev(k_norm)
@@ -54,6 +59,8 @@ def prefill_step(orc, seqs, seed, kv_dtype=q38a.KV_INT8, check_tokens=None):
     want = orc.attention_ragged(NQ, NKV, starts, b.seq_slot, b.tok_pos[sel], q16[sel], gate, NQ * HD, pool_host,
                                 kv_dtype, bt)
     want = bf16_bits_to_f32(want).reshape(len(sel), NQ * HD)
+    if return_out:
+        return got[sel], want
     return check_close(got[sel], want, what=f"prefill seqs={seqs}")
 
 
