@@ -288,10 +288,11 @@ OPROJ_COPIES = 14  # 14 x 20 MB of o-projection weights: more than the 256 MB MA
 def oproj_setup(name):
     """The attention layer's tail on a decode step (config 2 contexts for "o_proj_b8", 5a for
     "o_proj_long_b8"): split attention, then the o-projection (W_o 5,120 x 6,144, bq5) with the
-    residual epilogue. Returns (unfused(i), fused(i), gemm_only(i), facts). Unfused:
-    q38a_attention_decode (split kernel + merge kernel writing out), then q38a_qgemm on out. Fused:
-    q38a_attention_decode_partials, then q38a_qgemm_merge_oproj (the merge inside the GEMM's A
-    staging). Launch i uses KV pool i % 3 and weight copy i % OPROJ_COPIES."""
+    residual epilogue. Returns (unfused(i), in_loader(i), gemm_only(i), facts). Unfused:
+    q38a_attention_decode (split kernel + merge kernel writing out), then q38a_qgemm on out (what the
+    default q38a_qgemm_merge_oproj runs). In-loader: q38a_attention_decode_partials, then
+    q38a_qgemm_merge_oproj_in_loader (the merge inside the GEMM's A staging). Launch i uses KV pool
+    i % 3 and weight copy i % OPROJ_COPIES."""
     import torch
     import q38a
     from q38a import gemm
@@ -320,7 +321,7 @@ def oproj_setup(name):
 
     def fused(i):
         q38a.attention_decode_partials(ap, b.batch, descs[i % 3], s)
-        gemm.merge_oproj(ap, b.batch, ws_[i % OPROJ_COPIES][0], ep, ws, s)
+        gemm.merge_oproj(ap, b.batch, ws_[i % OPROJ_COPIES][0], ep, ws, s, in_loader=True)
 
     def gemm_only(i):
         gemm.qgemm(b.out.data_ptr(), B, ws_[i % OPROJ_COPIES][0], ep, ws, s)
@@ -348,8 +349,9 @@ def oproj_config(name, steps, warmup):
 
     t_u, t_f, t_g = timed(unfused), timed(fused), timed(gemm_only)
     return {"config": name, "B": B, "n": n, "k": K, "bits": 5, "weight_copies": OPROJ_COPIES,
-            "attention_plus_oproj_ms": round(t_u, 5), "fused_merge_oproj_ms": round(t_f, 5),
-            "oproj_gemm_only_ms": round(t_g, 5), "saved_ms": round(t_u - t_f, 5)}
+            "attention_plus_oproj_ms": round(t_u, 5), "in_loader_merge_oproj_ms": round(t_f, 5),
+            "oproj_gemm_only_ms": round(t_g, 5), "in_loader_saved_ms": round(t_u - t_f, 5),
+            "default": "merge kernel then GEMM (q38a_qgemm_merge_oproj)"}
 
 
 def runner_decode_config(steps, warmup, layers=16, ctxs=None, name="decode_b8_16_layers_runner"):
@@ -599,83 +601,117 @@ def read_mfma_busy():
     return out
 
 
-def cpu_baseline(batch, budget_s=20.0):
-    """Reference CPU attention (oracle/_ref: src/ref/ops.cpp attention_token) on the GPU batch's own
-    pages, single-threaded. Sequences are timed one after another until the budget is spent."""
+def cpu_sample(batch, picks, budget_s, cores):
+    """The oracle's C port of the reference's CPU attention (src/ref/ops.cpp:144-171, one query
+    token over its whole causal context, all 24 q heads) on picked query rows of a workload batch
+    whose append has run on the GPU, reading the batch's own pages. picks: [(row m, sequence b,
+    position)]. Each row is cut into its 4 kv heads (independent jobs); rows are timed one after
+    another on one thread until budget_s is spent, then the same rows are timed again spread over
+    `cores` threads (ctypes releases the GIL). Returns the sample's figures."""
     import numpy as np
-    import q38a
-    from oracle.oracle import REF_LIB, Oracle, Reference
-    kind = "reference" if os.path.exists(REF_LIB) else "port"
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle.oracle import Oracle
     orc = Oracle()
     pool = batch.pools[0].cpu().numpy()
-    q16 = batch.q16.cpu().numpy().view(np.uint16).reshape(batch.B, 24, 256)
-    gate = batch.proj.cpu().view(__import__("torch").int16).numpy().view(np.uint16)[:, 24 * 256:48 * 256]
+    q = batch.q16.cpu().float().numpy().reshape(-1, 24 * 256)
+    gate = batch.proj.cpu().float().numpy()[:, 24 * 256:48 * 256]
+    kv = {}
+    for _, b, pos in picks:
+        kv[b] = max(kv.get(b, 0), pos + 1)
+    kv = {b: orc.read_back(pool, batch.dtype, 4, batch.block_table, b, L) for b, L in kv.items()}
 
-    def f16_to_f32(h):
-        return np.asarray(h, np.uint16).view(np.float16).astype(np.float32)
+    def jobs_of(m, b, pos):
+        k, v = kv[b]
+        return [lambda h=h: orc.attention_token(q[m, 1536 * h:1536 * (h + 1)], gate[m, 1536 * h:1536 * (h + 1)], pos,
+                                                 k[h:h + 1, :pos + 1], v[h:h + 1, :pos + 1], 6, 1)
+                for h in range(4)]
 
-    def bf16_to_f32(b):
-        return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
-
-    ref = Reference() if kind == "reference" else None
-    done_tokens, done_bytes, spent = 0, 0, 0.0
-    order = sorted(range(batch.B), key=lambda b: batch.ctxs[b])
-    for b in order:
-        L = batch.ctxs[b] + 1
-        k, v = orc.read_back(pool, batch.dtype, 4, batch.block_table, b, L)
-        q = f16_to_f32(q16[b]).ravel()
-        g = bf16_to_f32(gate[b])
-        if kind == "reference":
-            st = ref.store(4, L)
-            st.k[...] = k
-            st.v[...] = v
-            t0 = time.perf_counter()
-            st.attention_token(24, q, g, L - 1)
-            dt = time.perf_counter() - t0
-            st.close()
-        else:
-            t0 = time.perf_counter()
-            orc.attention_token(q, g, L - 1, k, v, 24, 4)
-            dt = time.perf_counter() - t0
-        spent += dt
-        done_tokens += 1
-        done_bytes += L * (4096 if batch.dtype == q38a.KV_BF16 else 2112)
+    done, spent, keys = [], 0.0, 0
+    for m, b, pos in picks:
+        jobs = jobs_of(m, b, pos)
+        t0 = time.perf_counter()
+        for f in jobs:
+            f()
+        spent += time.perf_counter() - t0
+        done.append(jobs)
+        keys += pos + 1
         if spent > budget_s:
             break
-    out = {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-           "sample": f"{done_tokens} of {batch.B} decode rows (shortest first), one attention layer, "
-                     f"{done_bytes / 2112 if batch.dtype == 0 else done_bytes / 4096:.0f} KV tokens, "
-                     f"{spent:.2f} s single-threaded; tokens/s = {done_tokens / spent:.3f}",
-           "tokens_per_s": done_tokens / spent}
-    # The same rows again, one thread per row on the host's cores (the reference path is serial per
-    # token; rows are independent). ctypes releases the GIL during the call.
-    rows = order[:done_tokens]
-    cores = min(len(rows), len(os.sched_getaffinity(0)))
-    if cores > 1:
-        from concurrent.futures import ThreadPoolExecutor
-        jobs, stores = [], []
-        for b in rows:
-            L = batch.ctxs[b] + 1
-            k, v = orc.read_back(pool, batch.dtype, 4, batch.block_table, b, L)
-            q, g = f16_to_f32(q16[b]).ravel(), bf16_to_f32(gate[b])
-            if kind == "reference":
-                st = ref.store(4, L)
-                st.k[...] = k
-                st.v[...] = v
-                stores.append(st)
-                jobs.append(lambda st=st, q=q, g=g, p=L - 1: st.attention_token(24, q, g, p))
-            else:
-                jobs.append(lambda q=q, g=g, p=L - 1, k=k, v=v: orc.attention_token(q, g, p, k, v, 24, 4))
-        t0 = time.perf_counter()
-        with ThreadPoolExecutor(cores) as ex:
-            list(ex.map(lambda f: f(), jobs))
-        wall = time.perf_counter() - t0
-        for st in stores:
-            st.close()
-        out["all_cores"] = {"value": done_bytes / wall / 1e9, "cores": cores, "wall_s": round(wall, 3),
-                            "tokens_per_s": done_tokens / wall}
-    out["host"] = {"nproc": len(os.sched_getaffinity(0)), "cpu": cpu_model()}
-    return out
+    flat = [f for jobs in done for f in jobs]
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(cores) as ex:
+        list(ex.map(lambda f: f(), flat))
+    wall = time.perf_counter() - t0
+    per = 4096 if batch.dtype == 1 else 2112
+    n = len(done)
+    return {"rows": n, "of_picks": len(picks), "kv_tokens": keys, "s_1core": round(spent, 3),
+            "tokens_per_s_1core": round(n / spent, 3), "kv_gbs_1core": round(keys * per / spent / 1e9, 4),
+            "s_all_cores": round(wall, 3), "cores": cores, "tokens_per_s_all_cores": round(n / wall, 3),
+            "kv_gbs_all_cores": round(keys * per / wall / 1e9, 4),
+            "tflops_all_cores": round(keys * 4 * 256 * 24 / wall / 1e12, 6)}
+
+
+def cpu_baselines(head_batch):
+    """The reference CPU path timed on the host for every BASELINE config, on bounded samples (about
+    15 s of single-thread work in all); the headline cpu_baseline is config 2 (the bench workload),
+    all host cores."""
+    import numpy as np
+    import torch
+    import q38a
+    from q38a.workloads import DecodeBatch, RaggedBatch, decode_contexts, mixed_seqs
+    cores = len(os.sched_getaffinity(0))
+    s = torch.cuda.current_stream().cuda_stream
+    out = {}
+
+    def appended(b):
+        q38a.qk_norm_rope_append(b.append_params(), b.batch, b.kv_desc(0), s)
+        torch.cuda.synchronize()
+        return b
+
+    c1 = appended(DecodeBatch([130], seed=0))
+    r = cpu_sample(c1, [(0, 0, 130)] * 200, 2.0, cores)
+    r["sample"] = "config 1: one decode token at context 130, repeated 200 times"
+    out["config1_decode_ctx130"] = r
+    r = cpu_sample(head_batch, [(b, b, c) for b, c in sorted(enumerate(head_batch.ctxs), key=lambda x: x[1])],
+                   8.0, cores)
+    r["sample"] = "config 2: the bench's 8 decode rows, shortest first"
+    out["config2_decode_b8"] = r
+    c3 = appended(RaggedBatch([(6000, 2048)], seed=0))
+    toks = np.linspace(0, 2047, 48).astype(int)
+    r = cpu_sample(c3, [(int(t), 0, 6000 + int(t)) for t in toks], 4.0, cores)
+    pick_keys = [6001 + int(t) for t in toks[:r["rows"]]]
+    scale = sum(6001 + t for t in range(2048)) / sum(pick_keys)
+    r["est_full_chunk_s_1core"] = round(r["s_1core"] * scale, 2)
+    r["est_full_chunk_s_all_cores"] = round(r["s_all_cores"] * scale, 2)
+    r["sample"] = f"config 3: {r['rows']} of the chunk's 2,048 tokens, evenly spaced; full chunk scaled by keys"
+    out["config3_prefill_2048_on_6000"] = r
+    seqs = mixed_seqs(0)
+    c4 = appended(RaggedBatch(seqs, seed=0))
+    starts = np.cumsum([0] + [n for _, n in seqs])
+    pb = [b for b, (_, n) in enumerate(seqs) if n > 1][0]
+    p0, n0 = seqs[pb]
+    dec = [(int(starts[b]), b, p) for b, (p, n) in enumerate(seqs) if n == 1]
+    pre = [(int(starts[pb]) + int(t), pb, p0 + int(t)) for t in np.linspace(0, n0 - 1, 32).astype(int)]
+    r = cpu_sample(c4, dec + pre, 6.0, cores)
+    full_keys = sum(p + 1 for p, n in seqs if n == 1) + sum(p0 + t + 1 for t in range(n0))
+    sampled_keys = r["kv_tokens"]
+    r["est_full_step_s_1core"] = round(r["s_1core"] * full_keys / sampled_keys, 2)
+    r["est_full_step_s_all_cores"] = round(r["s_all_cores"] * full_keys / sampled_keys, 2)
+    r["sample"] = (f"config 4: the 7 decode rows and {max(0, r['rows'] - len(dec))} of the chunk's {n0} tokens; "
+                   "full step scaled by keys")
+    out["config4_mixed_512_plus_7"] = r
+    c5 = appended(DecodeBatch(decode_contexts("long_b8"), seed=0))
+    r = cpu_sample(c5, [(b, b, c) for b, c in sorted(enumerate(c5.ctxs), key=lambda x: x[1])], 6.0, cores)
+    r["sample"] = "config 5a: the 8 decode rows (contexts sum 204,800), shortest first"
+    out["config5a_long_b8"] = r
+    h = out["config2_decode_b8"]
+    return {"value": h["kv_gbs_all_cores"], "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"config 2 decode rows: {h['rows']} of 8, {h['kv_tokens']} KV tokens, one attention layer, "
+                      f"{h['s_all_cores']} s on {cores} threads (one job per row and kv head)",
+            "tokens_per_s": h["tokens_per_s_all_cores"],
+            "single_core": {"value": h["kv_gbs_1core"], "tokens_per_s": h["tokens_per_s_1core"], "s": h["s_1core"]},
+            "host": {"nproc": cores, "cpu": cpu_model()},
+            "configs": out}
 
 
 def cpu_model():
@@ -765,14 +801,16 @@ def main():
                 r["frac_of_same_bytes_ceiling"] = round(r["attn_gbs"] / ceil, 4)
         if "attn_tflops" in r:
             r["mfma_frac_of_measured"] = round(r["attn_tflops"] / peaks["mfma_fp16_tflops"], 4)
+    # MFMA-pipe busy fractions need hardware counters (rocprofv3 --pmc around this script), so they
+    # are read from the committed profile summaries and labelled as such
     busy = read_mfma_busy()
-    if busy and "prefill_2048_on_6000" in extra:
-        extra["prefill_2048_on_6000"]["mfma_busy_frac"] = busy.get("prefill")
-    if busy and "mixed_512_plus_7" in extra:
-        extra["mixed_512_plus_7"]["mfma_busy_frac"] = busy.get("mixed")
+    for w, key in (("prefill", "prefill_2048_on_6000"), ("mixed", "mixed_512_plus_7")):
+        if busy.get(w) is not None and key in extra:
+            extra[key]["mfma_busy_frac_from_profile"] = busy[w]
+            extra[key]["mfma_busy_source"] = f"profiles/attention_{w}_mfma.txt (rocprofv3 --pmc, not this run)"
     head_ceiling = read_ceiling(head["kv_bytes"])
     batch = head.pop("_batch")
-    cpu = None if args.no_cpu else cpu_baseline(batch)
+    cpu = None if args.no_cpu else cpu_baselines(batch)
     line = {
         "metric": "decode-attn KV GB/s (% HBM peak) + mixed-batch step tokens/s, batch 8",
         "value": round(head["kv_gbs"], 2),
@@ -792,6 +830,8 @@ def main():
                    "sum_ctx": sum(head["ctxs"]), "tokens_per_step": 8},
         "roofline": {"bound": "hbm", "achieved": round(head["attn_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["attn_gbs"] / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_b8"),
+                     "traffic_source": "profiles/attention_decode_b8_traffic.txt (rocprofv3 --pmc FETCH_SIZE / "
+                                       "WRITE_SIZE, not this run)",
                      "kernel": "attention_decode (attn_decode_kernel + attn_merge_kernel)",
                      "kernel_ms": round(head["attn_ms"], 5),
                      "measured_peak": peaks["hbm_read_gbs"],

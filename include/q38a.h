@@ -35,7 +35,10 @@ extern "C" {
  * the same bytes per page, K codes and K scales laid out as in INT8, but the V codes stored
  * transposed within each 16-token quarter of the page, [kvh][4 quarters][256 dims][16 tokens]
  * (a dim's 16 tokens contiguous, consecutive dims adjacent), and the V scales group-major,
- * [kvh][4 groups][64 tokens] f16. */
+ * [kvh][4 groups][64 tokens] f16.
+ * INT8_VT is EXPERIMENTAL: every kernel supports it and it is parity-tested like INT8, but it is
+ * slower than INT8 on every measured workload (decode, long-context decode, prefill and the mixed
+ * step), so INT8 is the format to use. */
 enum { Q38A_KV_INT8 = 0, Q38A_KV_BF16 = 1, Q38A_KV_INT8_VT = 2 };
 
 /* Status codes. */

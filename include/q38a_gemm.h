@@ -96,16 +96,22 @@ int q38a_qgemm_qkv_append(const uint16_t* a, int m, const q38a_bq_weight* w, con
                           const q38a_gemm_workspace* ws, const q38a_qk_norm_rope_params* append,
                           const q38a_batch_desc* batch, const q38a_kv_cache_desc* kv, void* stream);
 
-/* The attention layers' o-projection fed straight from the decode split partials (reference
- * OPTIMIZATION_PLAN.md:202-203, "attention split-merge into the o-projection's A loader"; unfused:
- * q38a_attention_decode's merge into attn->out, then qgemm on it, model_runner.cpp:351-357). A is
- * [B][nq * 256], A[b][256 h + d] the gated merge of decode row b's q head h, bit-identical to what
- * q38a_attention_decode writes into attn->out; attn and batch are those of the preceding
- * q38a_attention_decode_partials (same split scratch, same batch). For small batches the merge runs
- * in the GEMM's A staging and attn->out is not written; larger batches run the merge kernel into
- * attn->out and then the GEMM (attn->out must be set either way). w->k must be nq * 256. */
+/* The attention layers' o-projection after split-KV decode (unfused reference: the decode merge into
+ * attn->out, then qgemm on it, model_runner.cpp:351-357): attn and batch are those of the preceding
+ * q38a_attention_decode_partials (same split scratch, same batch); runs the gated merge kernel into
+ * attn->out, then q38a_qgemm with A = attn->out. w->k must be nq * 256. The result is bit-identical
+ * to q38a_attention_decode followed by q38a_qgemm. */
 int q38a_qgemm_merge_oproj(const q38a_attention_params* attn, const q38a_batch_desc* batch, const q38a_bq_weight* w,
                            const q38a_gemm_epilogue* ep, const q38a_gemm_workspace* ws, void* stream);
+
+/* As q38a_qgemm_merge_oproj, but for batches the small-M GEMM kernel takes (up to 32 rows) the merge
+ * runs inside the GEMM's A staging and attn->out is not written (reference OPTIMIZATION_PLAN.md:202-203,
+ * "attention split-merge into the o-projection's A loader"); larger batches as q38a_qgemm_merge_oproj.
+ * Same bits. Measured slower than the two launches at batch 8 (every GEMM workgroup repeats the merge
+ * of its A rows), so it is not the default. */
+int q38a_qgemm_merge_oproj_in_loader(const q38a_attention_params* attn, const q38a_batch_desc* batch,
+                                     const q38a_bq_weight* w, const q38a_gemm_epilogue* ep,
+                                     const q38a_gemm_workspace* ws, void* stream);
 
 /* Floats of split-K partials and counters q38a_qgemm / q38a_qgemm_qkv_append may use for an
  * (m, n, k) problem: out[0] partial floats, out[1] counters. */

@@ -34,6 +34,9 @@ _SIGS = {
     "q38a_qgemm_workspace_size": (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     "q38a_qgemm_merge_oproj": (_i, [ctypes.POINTER(AttentionParams), ctypes.POINTER(BatchDesc), ctypes.POINTER(BQWeight),
                                     ctypes.POINTER(GemmEpilogue), ctypes.POINTER(GemmWorkspace), _p]),
+    "q38a_qgemm_merge_oproj_in_loader": (_i, [ctypes.POINTER(AttentionParams), ctypes.POINTER(BatchDesc),
+                                              ctypes.POINTER(BQWeight), ctypes.POINTER(GemmEpilogue),
+                                              ctypes.POINTER(GemmWorkspace), _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -74,10 +77,11 @@ def qgemm(a_ptr, m, w, ep, ws, stream=0):
     _check(lib.q38a_qgemm(a_ptr, m, ctypes.byref(w), ctypes.byref(ep), ctypes.byref(ws), stream))
 
 
-def merge_oproj(attn, batch, w, ep, ws, stream=0):
-    """The o-projection straight from the decode split partials of attention_decode_partials."""
-    _check(lib.q38a_qgemm_merge_oproj(ctypes.byref(attn), ctypes.byref(batch), ctypes.byref(w), ctypes.byref(ep),
-                                      ctypes.byref(ws), stream))
+def merge_oproj(attn, batch, w, ep, ws, stream=0, in_loader=False):
+    """The o-projection after attention_decode_partials: the merge kernel then the GEMM, or with
+    in_loader the merge inside the small-M GEMM's A staging (same bits)."""
+    fn = lib.q38a_qgemm_merge_oproj_in_loader if in_loader else lib.q38a_qgemm_merge_oproj
+    _check(fn(ctypes.byref(attn), ctypes.byref(batch), ctypes.byref(w), ctypes.byref(ep), ctypes.byref(ws), stream))
 
 
 def qgemm_qkv_append(a_ptr, m, w, ep, ws, append, batch, kv, stream=0):

@@ -291,10 +291,12 @@ def test_in_projection_fused_append_matches_unfused(orc, seqs):
     pytest.param([20000, 513], 5120, id="b2_long"),
     pytest.param([40 + 37 * i for i in range(40)], 1024, id="b40_merge_kernel"),
 ])
-def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n):
-    """q38a_qgemm_merge_oproj (the merge inside the o-projection's A staging, or for more than 32
-    rows the merge kernel then the GEMM) equals q38a_attention_decode followed by q38a_qgemm on its
-    out, bit for bit in residual, xbf and partials_out; that GEMM against the oracle's."""
+@pytest.mark.parametrize("in_loader", [False, True])
+def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n, in_loader):
+    """q38a_qgemm_merge_oproj (the merge kernel then the GEMM) and q38a_qgemm_merge_oproj_in_loader
+    (the merge inside the o-projection's A staging, or for more than 32 rows as the former) equal
+    q38a_attention_decode followed by q38a_qgemm on its out, bit for bit in residual, xbf and
+    partials_out; that GEMM against the oracle's."""
     from gpu_util import attention_params
     from util import randn_bf16
     rng = np.random.default_rng(77)
@@ -327,7 +329,7 @@ def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n):
                                0, 1e-6)
         if fused:
             q38a.attention_decode_partials(attn, b.desc, pool.desc, stream())
-            gemm.merge_oproj(attn, b.desc, w.desc, ep, ws, stream())
+            gemm.merge_oproj(attn, b.desc, w.desc, ep, ws, stream(), in_loader=in_loader)
         else:
             q38a.attention_decode(attn, b.desc, pool.desc, stream())
             gemm.qgemm(out_t.data_ptr(), B, w.desc, ep, ws, stream())
@@ -339,7 +341,7 @@ def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n):
     assert_bits_equal(r_f, r_u, "residual")
     assert_bits_equal(x_f, x_u, "xbf")
     assert_bits_equal(p_f, p_u, "partials_out")
-    if B > 32:  # the merge kernel wrote out on the fused path too
+    if B > 32 or not in_loader:  # the merge kernel wrote out
         assert_bits_equal(a_f, a_u, "out")
     a = a_u.reshape(B, NQ * HD)
     check_residual(orc, w, a, res0, r_u.reshape(B, n), x_u.reshape(B, n), p_u.reshape(B, n // 128))
