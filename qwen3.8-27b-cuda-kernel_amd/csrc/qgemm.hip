@@ -132,12 +132,10 @@ __device__ inline void load_bwords(BWords& b, const BPlanes& p, int nb, int g, i
   b.scale = __builtin_amdgcn_raw_buffer_load_b16(p.sc, (lane & 31) * 2, unit * 64, 0);
 }
 
-// (x & m) | c in one instruction (v_and_or_b32; m and c wave-uniform)
-__device__ inline uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
-  return r;
-}
+// (x & m) | c: one v_and_or_b32. Plain code, not inline assembly: an MFMA reading a register that an
+// inline-assembly instruction wrote gets no hazard wait states from the compiler (it does not count
+// the assembly as a VALU write), and then reads stale values.
+__device__ inline uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
 
 // Shift right by a signed constant (left when negative).
 template <int R>
@@ -924,6 +922,105 @@ qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn mi) 
   tile_finish<1, FUSED, EV>(a, ap, batch, kv, sh, C, tile, z, tn, wave, lane);
 }
 
+// ---- decode-size M (<= 8 rows) on a wide column grid: 64-column tiles over the whole K --------------
+// One 16-wave workgroup per 64-column tile (the in-projection: 224 tiles for 256 CUs), each wave over
+// 1/16 of the K groups for both 32-column blocks of the tile, with the next group's A rows and weights
+// in flight while it computes the current one. No split-K crosses workgroups: the 16 waves' sums are
+// added in LDS in wave order (deterministic) and the workgroup stores its tile. A rows go straight
+// from global memory into the MFMA operands (rows >= M load as zero without a memory request). Only
+// the 4 MFMA output elements per lane that can hold rows < 8 take the per-group epilogue arithmetic.
+// StoreBF16 / StoreF32 only (the residual epilogue's 128-column sums of squares would span two
+// tiles).
+constexpr int kWideWaves = 16;
+constexpr int kWideCols = 64;
+constexpr int kWideRows = 8;
+
+struct alignas(16) WideShared {
+  float c[kWideWaves][2][4][64];  // per wave: block, element (rows 4 kg + e), lane
+  float rs[kWideRows];
+};
+
+template <int BITS>
+__global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a) {
+  __shared__ WideShared sh;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, kg = lane >> 5;
+  const int tn = blockIdx.x;
+  const int G = a.k / 64;
+  const int g0 = wave * G / kWideWaves, g1 = (wave + 1) * G / kWideWaves;
+  const int nb0 = tn * (kWideCols / 32);
+  // the row scales before any weight load: a branch over outstanding loads would make the waits
+  // conservative
+  if (threadIdx.x < kWideRows) sh.rs[threadIdx.x] = row_scale(a, threadIdx.x);
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(const_cast<uint16_t*>(a.a)), short(0), a.m * a.k * int(sizeof(uint16_t)), 0x00020000);
+  const BPlanes bp = make_bplanes<BITS>(a);
+  const int aoff = ((lane & 31) * a.k + 8 * kg) * int(sizeof(uint16_t));
+  const float c0 = 128.0f + float(1 << (BITS - 1));
+  const uint32_t magic = 0x43004300u;
+  bf16x8_t ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = __bf16(1.0f);
+  float C[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) C[j][e] = 0.0f;
+  // two register buffers rotate over the groups (three measured slower: 18.7 vs 17.5 us, as was
+  // issuing every group's weights at once with the A rows staged in LDS, 19.2 us)
+  constexpr int kDepth = 2;
+  u32x4 A[kDepth][1][4];
+  BWords B[kDepth][2];
+  auto load_group = [&](u32x4 (&Ab)[1][4], BWords (&Bb)[2], int g) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      Ab[0][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff, (64 * g + 16 * s) * 2, 0));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_bwords<BITS>(Bb[j], bp, nb0 + j, g, G, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute_group = [&](const u32x4 (&Ab)[1][4], const BWords (&Bb)[2], bool take) {
+    float16_t S;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, Ab[0][s]), ones, s == 0 ? float16_t{} : S, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float16_t T[1];
+      group_products<BITS, 1>(T, Ab, Bb[j], magic);
+      const float sc = take ? bf16_value(uint16_t(Bb[j].scale)) : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) C[j][e] = __builtin_fmaf(sc, __builtin_fmaf(-c0, S[e], T[0][e]), C[j][e]);
+    }
+  };
+  const int glast = g1 - 1;
+  auto gc = [&](int g) { return g < glast ? g : glast; };
+#pragma unroll
+  for (int d = 0; d + 1 < kDepth; ++d) load_group(A[d], B[d], gc(g0 + d));
+  for (int g = g0; g < g1; g += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      load_group(A[(d + kDepth - 1) % kDepth], B[(d + kDepth - 1) % kDepth], gc(g + d + kDepth - 1));
+      compute_group(A[d], B[d], g + d < g1);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sh.c[wave][j][e][lane] = C[j][e];
+  __syncthreads();
+  if (threadIdx.x >= 2 * 4 * 64) return;
+  const int t = threadIdx.x, j = t >> 8, e = (t >> 6) & 3, l = t & 63;
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWideWaves; ++w) v += sh.c[w][j][e][l];
+  const int row = 4 * (l >> 5) + e, col = tn * kWideCols + 32 * j + (l & 31);
+  if (row >= a.m || col >= a.n_store) return;
+  const float y = v * sh.rs[row];
+  if (a.kind == Q38A_EPI_STORE_F32) static_cast<float*>(a.out)[size_t(row) * a.ldo + col] = y;
+  else static_cast<uint16_t*>(a.out)[size_t(row) * a.ldo + col] = bf16_bits(y);
+}
+
 // Split-K plan. Small M (qgemv_kernel, one 1024-thread workgroup per CU): slices of at most
 // kSliceG groups (the staged A), and at most as many as fill the CUs once without a second round;
 // each of the two K parts keeps a group. Larger M (qgemm_kernel): enough workgroups to stream the weights at
@@ -1057,6 +1154,21 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
       case 4: hipLaunchKernelGGL((qgemm_big_kernel<4>), bgrid, bblock, 0, stream, g); break;
       case 5: hipLaunchKernelGGL((qgemm_big_kernel<5>), bgrid, bblock, 0, stream, g); break;
       case 6: hipLaunchKernelGGL((qgemm_big_kernel<6>), bgrid, bblock, 0, stream, g); break;
+      default: return set_error(Q38A_ERR_UNSUPPORTED, "qgemm: %d-bit weights are not supported", w.bits);
+    }
+    if (int rc = check_hip(hipGetLastError(), "qgemm launch")) return rc;
+    return mode == 1 ? launch_qk_norm_rope_append(*ap, *b, *kv, stream) : Q38A_OK;
+  }
+  // decode-size M with a store epilogue on a wide weight: the 64-column-tile kernel, no split-K. With
+  // the append requested, that GEMM and then the append launch (the same bits as the two calls).
+  const int wide_tiles = w.n / kWideCols;
+  if (m <= kWideRows && mode != 2 && ep.kind != Q38A_EPI_RESIDUAL && wide_tiles >= (3 * cus) / 4 &&
+      w.k / 64 >= kWideWaves) {
+    if (mode == 1) g.kind = ep.kind;
+    switch (w.bits) {
+      case 4: hipLaunchKernelGGL((qgemv_wide_kernel<4>), dim3(unsigned(wide_tiles)), dim3(64 * kWideWaves), 0, stream, g); break;
+      case 5: hipLaunchKernelGGL((qgemv_wide_kernel<5>), dim3(unsigned(wide_tiles)), dim3(64 * kWideWaves), 0, stream, g); break;
+      case 6: hipLaunchKernelGGL((qgemv_wide_kernel<6>), dim3(unsigned(wide_tiles)), dim3(64 * kWideWaves), 0, stream, g); break;
       default: return set_error(Q38A_ERR_UNSUPPORTED, "qgemm: %d-bit weights are not supported", w.bits);
     }
     if (int rc = check_hip(hipGetLastError(), "qgemm launch")) return rc;

@@ -174,6 +174,48 @@ def test_qgemm_residual(orc, m):
 
 
 @pytest.mark.parametrize("bits", [4, 5, 6])
+@pytest.mark.parametrize("m,kind", [(1, "bf16"), (5, "f32"), (8, "bf16"), (8, "f32")])
+def test_qgemm_decode_rows_wide_tiles(orc, bits, m, kind):
+    """Up to 8 rows on a weight wide enough for the 64-column-tile kernel (no split-K; the in-projection
+    shape, 14,336 x 5,120): against the oracle, and bit for bit across repeated launches (its waves'
+    sums are added in a fixed order)."""
+    n, k = 14336, 5120
+    w = Weight(orc, bits, n, k, seed=60 + bits, scale_lo=0.0005, scale_hi=0.004)
+    rng = np.random.default_rng(61 + m)
+    a = randn_bf16(rng, (m, k), 3.0)
+    a_t = dev(a)
+    ws, keep = workspace(m, n, k)
+    wo, wmag = oracle_weight(w, m)
+    print(f"qgemm wide tiles: bits={bits} m={m} kind={kind}", flush=True)
+    outs = []
+    for rep in range(3):
+        if kind == "f32":
+            n_store = n - 100
+            out = torch.full((m * n,), float("nan"), dtype=torch.float32, device="cuda")
+            ep = gemm.GemmEpilogue(gemm.EPI_STORE_F32, out.data_ptr(), n, n_store, None, None, None, None, 0, 1e-6)
+        else:
+            partials = rng.uniform(2000.0, 9000.0, (m, k // 128)).astype(np.float32) if rep == 0 else partials
+            p_t = dev(partials)
+            out = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+            ep = gemm.GemmEpilogue(gemm.EPI_STORE_BF16, out.data_ptr(), n, 0, None, None, None, p_t.data_ptr(), k, 1e-6)
+        gemm.qgemm(a_t.data_ptr(), m, w.desc, ep, ws, stream())
+        torch.cuda.synchronize()
+        outs.append(host(out) if kind == "f32" else host(out, np.uint16))
+    for o in outs[1:]:
+        assert_bits_equal(o.view(np.uint32) if kind == "f32" else o, outs[0].view(np.uint32) if kind == "f32" else outs[0],
+                          "repeated launch")
+    if kind == "f32":
+        got = outs[0].reshape(m, n)
+        want = orc.qgemm(a, wo, 3, n_store=n_store)
+        close(got[:, :n_store], want[:, :n_store], "wide f32", a, wmag[:n_store], out="f32")
+        assert np.isnan(got[:, n_store:]).all()
+    else:
+        got = bf16_bits_to_f32(outs[0]).reshape(m, n)
+        want = bf16_bits_to_f32(orc.qgemm(a, wo, 0, partials_in=partials, hidden=k))
+        close(got, want, "wide bf16", a, wmag, row_scales(partials, k))
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6])
 @pytest.mark.parametrize("kind", ["bf16", "f32", "residual"])
 def test_qgemm_large_m_tiles(orc, bits, kind):
     """Large M with enough 256 x 256 tiles to fill the CUs: the kernel that dequantises each weight
