@@ -121,15 +121,18 @@ __device__ inline BPlanes make_bplanes(const GemmArgs& a) {
   return p;
 }
 
-template <int BITS>
+// Cache policy of a buffer load: non-temporal (data read once).
+constexpr int kNonTemporal = 2;
+
+template <int BITS, int CPOL = 0>
 __device__ inline void load_bwords(BWords& b, const BPlanes& p, int nb, int g, int G, int lane) {
   const int unit = nb * G + g;
-  b.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(p.lo, lane * 16, unit * 1024, 0));
-  if constexpr (BITS == 5) b.hi = u32x2{__builtin_amdgcn_raw_buffer_load_b32(p.hi, lane * 4, unit * 256, 0), 0u};
+  b.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(p.lo, lane * 16, unit * 1024, CPOL));
+  if constexpr (BITS == 5) b.hi = u32x2{__builtin_amdgcn_raw_buffer_load_b32(p.hi, lane * 4, unit * 256, CPOL), 0u};
   else if constexpr (BITS == 6)
-    b.hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(p.hi, lane * 8, unit * 512, 0));
+    b.hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(p.hi, lane * 8, unit * 512, CPOL));
   else b.hi = u32x2{0u, 0u};
-  b.scale = __builtin_amdgcn_raw_buffer_load_b16(p.sc, (lane & 31) * 2, unit * 64, 0);
+  b.scale = __builtin_amdgcn_raw_buffer_load_b16(p.sc, (lane & 31) * 2, unit * 64, CPOL);
 }
 
 // (x & m) | c: one v_and_or_b32. Plain code, not inline assembly: an MFMA reading a register that an
@@ -923,21 +926,37 @@ qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn mi) 
 }
 
 // ---- decode-size M (<= 8 rows) on a wide column grid: 64-column tiles over the whole K --------------
-// One 16-wave workgroup per 64-column tile (the in-projection: 224 tiles for 256 CUs), each wave over
-// 1/16 of the K groups for both 32-column blocks of the tile, with the next group's A rows and weights
-// in flight while it computes the current one. No split-K crosses workgroups: the 16 waves' sums are
-// added in LDS in wave order (deterministic) and the workgroup stores its tile. A rows go straight
-// from global memory into the MFMA operands (rows >= M load as zero without a memory request). Only
-// the 4 MFMA output elements per lane that can hold rows < 8 take the per-group epilogue arithmetic.
-// StoreBF16 / StoreF32 only (the residual epilogue's 128-column sums of squares would span two
-// tiles).
-constexpr int kWideWaves = 16;
+// One 8-wave workgroup per 64-column tile (the in-projection: 224 tiles for 256 CUs). The tile's K
+// groups are cut into fixed chunks (two or three groups, both 32-column blocks); the waves take
+// chunks from a counter in LDS as they finish, so a wave that the memory system serves late takes
+// fewer (with a fixed share of K per wave, the workgroup waited ~4 us for its slowest wave after the
+// mean wave was done). Each chunk's sums go to its own LDS slot and the slots are added in chunk
+// order: the result does not depend on which wave took which chunk. A wave keeps its next group in
+// flight across chunk boundaries (it claims the next chunk when it issues that chunk's first
+// loads). A group's A rows come in one 16-byte load per lane (8 rows x 64 k, rows >= M load as
+// zero) and pass through the wave's LDS buffer into the MFMA operand layout (loaded straight into
+// that layout, 48 of a load's 64 lanes held rows >= 8, four loads per group). Weights are loaded
+// non-temporal (read once). Only the 4 MFMA output elements per lane that can hold rows < 8 take
+// the per-group epilogue arithmetic. StoreBF16 / StoreF32 only (the residual epilogue's 128-column
+// sums of squares would span two tiles).
+//
+// Measured on the in-projection at M = 8 (HIP events, weights rotating through 8 copies): 17.1 us
+// with a fixed share of K per wave and A loaded into the operand layout; 16.1 with the chunk
+// claims; 15.0 with the compact A loads and non-temporal weights; 14.7 with 8 waves instead of 16.
+// More groups in flight per wave (3 or 4), or 4 waves with 4 in flight, were slower (16-19 us), as
+// was staging all of A in LDS once per workgroup (17.4 us).
+constexpr int kWideWaves = 8;
 constexpr int kWideCols = 64;
 constexpr int kWideRows = 8;
+constexpr int kWideMaxChunks = 40;
+
+__host__ __device__ constexpr int wide_chunks(int G) { return G / 2 < kWideMaxChunks ? G / 2 : kWideMaxChunks; }
 
 struct alignas(16) WideShared {
-  float c[kWideWaves][2][4][64];  // per wave: block, element (rows 4 kg + e), lane
+  u32x4 a[kWideWaves][2][8][8];  // per wave and buffer: the group's A rows, [k chunk][row]
+  float c[kWideMaxChunks][2][4][64];  // per chunk: block, element (rows 4 kg + e), lane
   float rs[kWideRows];
+  int next;  // the next unclaimed chunk
 };
 
 template <int BITS>
@@ -947,15 +966,18 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
   const int lane = threadIdx.x & 63, kg = lane >> 5;
   const int tn = blockIdx.x;
   const int G = a.k / 64;
-  const int g0 = wave * G / kWideWaves, g1 = (wave + 1) * G / kWideWaves;
+  const int NC = wide_chunks(G);
   const int nb0 = tn * (kWideCols / 32);
-  // the row scales before any weight load: a branch over outstanding loads would make the waits
-  // conservative
+  // the counter's first value before any wave claims, and the row scales before any weight load (a
+  // branch over outstanding loads would make the waits conservative)
+  if (threadIdx.x == 0) sh.next = kWideWaves;
+  __syncthreads();
   if (threadIdx.x < kWideRows) sh.rs[threadIdx.x] = row_scale(a, threadIdx.x);
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       uniform_ptr(const_cast<uint16_t*>(a.a)), short(0), a.m * a.k * int(sizeof(uint16_t)), 0x00020000);
   const BPlanes bp = make_bplanes<BITS>(a);
-  const int aoff = ((lane & 31) * a.k + 8 * kg) * int(sizeof(uint16_t));
+  // compact A loads: lane = 8 chunk + row (every lane useful; rows >= M load as zero)
+  const int aoff = ((lane & 7) * a.k + 8 * (lane >> 3)) * int(sizeof(uint16_t));
   const float c0 = 128.0f + float(1 << (BITS - 1));
   const uint32_t magic = 0x43004300u;
   bf16x8_t ones;
@@ -966,20 +988,37 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) C[j][e] = 0.0f;
-  // two register buffers rotate over the groups (three measured slower: 18.7 vs 17.5 us, as was
-  // issuing every group's weights at once with the A rows staged in LDS, 19.2 us)
+  auto chunk_begin = [&](int c) { return c * G / NC; };
+  // load cursor (wave-uniform): chunk lc (>= NC once the chunks are gone), group lg of it
+  int lc = wave, lg = chunk_begin(wave), lend = chunk_begin(wave + 1);
+  // two register buffers rotate over the groups
   constexpr int kDepth = 2;
-  u32x4 A[kDepth][1][4];
+  u32x4 A[kDepth];
   BWords B[kDepth][2];
-  auto load_group = [&](u32x4 (&Ab)[1][4], BWords (&Bb)[2], int g) {
+  int rc[kDepth], rg[kDepth];  // chunk and group in each buffer (wave-uniform)
+  auto load_next = [&](int d) {
+    if (lc < NC && lg == lend) {
+      int c = 0;
+      if (lane == 0) c = atomicAdd(&sh.next, 1);
+      lc = __builtin_amdgcn_readfirstlane(c);
+      if (lc < NC) { lg = chunk_begin(lc); lend = chunk_begin(lc + 1); }
+    }
+    const int g = lc < NC ? lg : G - 1;  // past the last chunk: a valid address, never used
+    rc[d] = lc;
+    rg[d] = lg;
+    A[d] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff, 128 * g, 0));
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      Ab[0][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff, (64 * g + 16 * s) * 2, 0));
-#pragma unroll
-    for (int j = 0; j < 2; ++j) load_bwords<BITS>(Bb[j], bp, nb0 + j, g, G, lane);
+    for (int j = 0; j < 2; ++j) load_bwords<BITS, kNonTemporal>(B[d][j], bp, nb0 + j, g, G, lane);
     __builtin_amdgcn_sched_barrier(0);
+    ++lg;
   };
-  auto compute_group = [&](const u32x4 (&Ab)[1][4], const BWords (&Bb)[2], bool take) {
+  auto compute = [&](int d) {
+    // through the wave's LDS buffer into the operand layout: row lane % 32 (rows >= 8 repeat rows
+    // 0-7; their output rows are never read), k chunk 2 s + lane / 32
+    sh.a[wave][d][lane >> 3][lane & 7] = A[d];
+    u32x4 Ab[1][4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) Ab[0][s] = sh.a[wave][d][2 * s + kg][lane & 7];
     float16_t S;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
@@ -987,33 +1026,36 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       float16_t T[1];
-      group_products<BITS, 1>(T, Ab, Bb[j], magic);
-      const float sc = take ? bf16_value(uint16_t(Bb[j].scale)) : 0.0f;
+      group_products<BITS, 1>(T, Ab, B[d][j], magic);
+      const float sc = bf16_value(uint16_t(B[d][j].scale));
 #pragma unroll
       for (int e = 0; e < 4; ++e) C[j][e] = __builtin_fmaf(sc, __builtin_fmaf(-c0, S[e], T[0][e]), C[j][e]);
     }
-  };
-  const int glast = g1 - 1;
-  auto gc = [&](int g) { return g < glast ? g : glast; };
+    if (rg[d] + 1 == chunk_begin(rc[d] + 1)) {  // the chunk's last group: its sums to its slot
 #pragma unroll
-  for (int d = 0; d + 1 < kDepth; ++d) load_group(A[d], B[d], gc(g0 + d));
-  for (int g = g0; g < g1; g += kDepth) {
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      load_group(A[(d + kDepth - 1) % kDepth], B[(d + kDepth - 1) % kDepth], gc(g + d + kDepth - 1));
-      compute_group(A[d], B[d], g + d < g1);
+        for (int e = 0; e < 4; ++e) {
+          sh.c[rc[d]][j][e][lane] = C[j][e];
+          C[j][e] = 0.0f;
+        }
     }
+  };
+  load_next(0);
+  for (;;) {
+    load_next(1);
+    if (rc[0] >= NC) break;
+    compute(0);
+    load_next(0);
+    if (rc[1] >= NC) break;
+    compute(1);
   }
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sh.c[wave][j][e][lane] = C[j][e];
   __syncthreads();
-  if (threadIdx.x >= 2 * 4 * 64) return;
+  // one thread per (block, element, lane): the chunks' sums in chunk order
+  static_assert(kWideWaves * 64 == 2 * 4 * 64, "one thread per output element");
   const int t = threadIdx.x, j = t >> 8, e = (t >> 6) & 3, l = t & 63;
   float v = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kWideWaves; ++w) v += sh.c[w][j][e][l];
+  for (int c = 0; c < NC; ++c) v += sh.c[c][j][e][l];
   const int row = 4 * (l >> 5) + e, col = tn * kWideCols + 32 * j + (l & 31);
   if (row >= a.m || col >= a.n_store) return;
   const float y = v * sh.rs[row];
@@ -1163,7 +1205,7 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
   // the append requested, that GEMM and then the append launch (the same bits as the two calls).
   const int wide_tiles = w.n / kWideCols;
   if (m <= kWideRows && mode != 2 && ep.kind != Q38A_EPI_RESIDUAL && wide_tiles >= (3 * cus) / 4 &&
-      w.k / 64 >= kWideWaves) {
+      wide_chunks(w.k / 64) >= kWideWaves) {
     if (mode == 1) g.kind = ep.kind;
     switch (w.bits) {
       case 4: hipLaunchKernelGGL((qgemv_wide_kernel<4>), dim3(unsigned(wide_tiles)), dim3(64 * kWideWaves), 0, stream, g); break;
