@@ -107,8 +107,11 @@ int q38a_qgemm_merge_oproj(const q38a_attention_params* attn, const q38a_batch_d
 /* As q38a_qgemm_merge_oproj, but for batches the small-M GEMM kernel takes (up to 32 rows) the merge
  * runs inside the GEMM's A staging and attn->out is not written (reference OPTIMIZATION_PLAN.md:202-203,
  * "attention split-merge into the o-projection's A loader"); larger batches as q38a_qgemm_merge_oproj.
- * Same bits. Measured slower than the two launches at batch 8 (every GEMM workgroup repeats the merge
- * of its A rows), so it is not the default. */
+ * The merged A rows are the merge kernel's bits, but the GEMM is the split-K kernel, so at <= 8 rows
+ * (where q38a_qgemm takes the wide-tile kernel) the results differ from q38a_qgemm_merge_oproj's in
+ * the fp32 summation order (both within the GEMM's tolerance of the exact product). Measured slower
+ * than the two launches at batch 8 (every GEMM workgroup repeats the merge of its A rows), so it is
+ * not the default. */
 int q38a_qgemm_merge_oproj_in_loader(const q38a_attention_params* attn, const q38a_batch_desc* batch,
                                      const q38a_bq_weight* w, const q38a_gemm_epilogue* ep,
                                      const q38a_gemm_workspace* ws, void* stream);

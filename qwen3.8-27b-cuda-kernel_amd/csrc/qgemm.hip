@@ -946,33 +946,46 @@ qgemv_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn mi) 
 // More groups in flight per wave (3 or 4), or 4 waves with 4 in flight, were slower (16-19 us), as
 // was staging all of A in LDS once per workgroup (17.4 us).
 constexpr int kWideWaves = 8;
-constexpr int kWideCols = 64;
 constexpr int kWideRows = 8;
-constexpr int kWideMaxChunks = 40;
+constexpr int kWideSlotFloats = 40 * 2 * 4 * 64;  // the chunks' sums in LDS (80 KB)
+constexpr int kWideMaxSplits = 8;
 
-__host__ __device__ constexpr int wide_chunks(int G) { return G / 2 < kWideMaxChunks ? G / 2 : kWideMaxChunks; }
+// Chunks of a workgroup's Gs groups for tiles of nb 32-column blocks: at most as many as fill the
+// LDS slots (40 of two blocks, 20 of four), at least one group each.
+__host__ __device__ constexpr int wide_chunks(int nb, int gs) {
+  return gs < kWideSlotFloats / (nb * 256) ? gs : kWideSlotFloats / (nb * 256);
+}
 
 struct alignas(16) WideShared {
   u32x4 a[kWideWaves][2][8][8];  // per wave and buffer: the group's A rows, [k chunk][row]
-  float c[kWideMaxChunks][2][4][64];  // per chunk: block, element (rows 4 kg + e), lane
+  float c[kWideSlotFloats];      // per chunk: [block][element (rows 4 kg + e)][lane]
   float rs[kWideRows];
-  int next;  // the next unclaimed chunk
+  float ss[kWideWaves][2];       // residual epilogue: per wave, its two rows' sums of squares
+  int next;                      // the next unclaimed chunk
+  int last;                      // split-K: this workgroup arrived last
 };
 
-template <int BITS>
+// NB: 32-column blocks per tile (2: StoreBF16 / StoreF32; 4: the residual epilogue, whose tile is
+// one 128-column block of the sums of squares). gridDim.y: K splits; with more than one, every
+// split writes its tile sums (write-through, as in the split-K kernel) and the last to arrive adds
+// them in split order and runs the epilogue.
+template <int BITS, int NB, bool RES>
 __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a) {
+  static_assert(!RES || NB == 4, "the residual epilogue needs 128-column tiles");
+  constexpr int kOut = NB * 4 * 64 / (64 * kWideWaves);  // output values per thread
   __shared__ WideShared sh;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, kg = lane >> 5;
-  const int tn = blockIdx.x;
+  const int tn = blockIdx.x, ks = blockIdx.y, KS = gridDim.y;
   const int G = a.k / 64;
-  const int NC = wide_chunks(G);
-  const int nb0 = tn * (kWideCols / 32);
+  const int gb = ks * G / KS, Gs = (ks + 1) * G / KS - gb;
+  const int NC = wide_chunks(NB, Gs);
+  const int nb0 = tn * NB;
   // the counter's first value before any wave claims, and the row scales before any weight load (a
   // branch over outstanding loads would make the waits conservative)
   if (threadIdx.x == 0) sh.next = kWideWaves;
   __syncthreads();
-  if (threadIdx.x < kWideRows) sh.rs[threadIdx.x] = row_scale(a, threadIdx.x);
+  if (!RES && threadIdx.x < kWideRows) sh.rs[threadIdx.x] = row_scale(a, threadIdx.x);
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       uniform_ptr(const_cast<uint16_t*>(a.a)), short(0), a.m * a.k * int(sizeof(uint16_t)), 0x00020000);
   const BPlanes bp = make_bplanes<BITS>(a);
@@ -983,18 +996,18 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
   bf16x8_t ones;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ones[i] = __bf16(1.0f);
-  float C[2][4];
+  float C[NB][4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) C[j][e] = 0.0f;
-  auto chunk_begin = [&](int c) { return c * G / NC; };
+  auto chunk_begin = [&](int c) { return gb + c * Gs / NC; };
   // load cursor (wave-uniform): chunk lc (>= NC once the chunks are gone), group lg of it
   int lc = wave, lg = chunk_begin(wave), lend = chunk_begin(wave + 1);
   // two register buffers rotate over the groups
   constexpr int kDepth = 2;
   u32x4 A[kDepth];
-  BWords B[kDepth][2];
+  BWords B[kDepth][NB];
   int rc[kDepth], rg[kDepth];  // chunk and group in each buffer (wave-uniform)
   auto load_next = [&](int d) {
     if (lc < NC && lg == lend) {
@@ -1003,12 +1016,12 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
       lc = __builtin_amdgcn_readfirstlane(c);
       if (lc < NC) { lg = chunk_begin(lc); lend = chunk_begin(lc + 1); }
     }
-    const int g = lc < NC ? lg : G - 1;  // past the last chunk: a valid address, never used
+    const int g = lc < NC ? lg : gb;  // past the last chunk: a valid address, never used
     rc[d] = lc;
     rg[d] = lg;
     A[d] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff, 128 * g, 0));
 #pragma unroll
-    for (int j = 0; j < 2; ++j) load_bwords<BITS, kNonTemporal>(B[d][j], bp, nb0 + j, g, G, lane);
+    for (int j = 0; j < NB; ++j) load_bwords<BITS, kNonTemporal>(B[d][j], bp, nb0 + j, g, G, lane);
     __builtin_amdgcn_sched_barrier(0);
     ++lg;
   };
@@ -1024,7 +1037,7 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
     for (int s = 0; s < 4; ++s)
       S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, Ab[0][s]), ones, s == 0 ? float16_t{} : S, 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NB; ++j) {
       float16_t T[1];
       group_products<BITS, 1>(T, Ab, B[d][j], magic);
       const float sc = bf16_value(uint16_t(B[d][j].scale));
@@ -1032,11 +1045,12 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
       for (int e = 0; e < 4; ++e) C[j][e] = __builtin_fmaf(sc, __builtin_fmaf(-c0, S[e], T[0][e]), C[j][e]);
     }
     if (rg[d] + 1 == chunk_begin(rc[d] + 1)) {  // the chunk's last group: its sums to its slot
+      float* slot = sh.c + rc[d] * (NB * 256);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          sh.c[rc[d]][j][e][lane] = C[j][e];
+          slot[(4 * j + e) * 64 + lane] = C[j][e];
           C[j][e] = 0.0f;
         }
     }
@@ -1051,16 +1065,118 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
     compute(1);
   }
   __syncthreads();
-  // one thread per (block, element, lane): the chunks' sums in chunk order
-  static_assert(kWideWaves * 64 == 2 * 4 * 64, "one thread per output element");
-  const int t = threadIdx.x, j = t >> 8, e = (t >> 6) & 3, l = t & 63;
-  float v = 0.0f;
-  for (int c = 0; c < NC; ++c) v += sh.c[c][j][e][l];
-  const int row = 4 * (l >> 5) + e, col = tn * kWideCols + 32 * j + (l & 31);
-  if (row >= a.m || col >= a.n_store) return;
-  const float y = v * sh.rs[row];
-  if (a.kind == Q38A_EPI_STORE_F32) static_cast<float*>(a.out)[size_t(row) * a.ldo + col] = y;
-  else static_cast<uint16_t*>(a.out)[size_t(row) * a.ldo + col] = bf16_bits(y);
+  // output value i of this thread: index x = t + 512 i = (block j, element e, lane l); the chunks'
+  // sums in chunk order
+  const int t = threadIdx.x;
+  float v[kOut];
+#pragma unroll
+  for (int i = 0; i < kOut; ++i) {
+    float x = 0.0f;
+    for (int c = 0; c < NC; ++c) x += sh.c[c * (NB * 256) + t + 64 * kWideWaves * i];
+    v[i] = x;
+  }
+  if (KS > 1) {
+    // the tile's K splits: write-through partials, an arrival count, the last arrival sums them in
+    // split order with agent-coherent loads (the hand-off of the split-K kernel, tile_finish)
+    float* part = a.ws_partials + size_t(tn) * KS * (NB * 256);
+#pragma unroll
+    for (int i = 0; i < kOut; ++i)
+      __hip_atomic_store(part + ks * (NB * 256) + t + 64 * kWideWaves * i, v[i], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the write-through stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int old = __hip_atomic_fetch_add(a.counters + tn, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sh.last = old == KS - 1;
+      if (sh.last) __hip_atomic_store(a.counters + tn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!sh.last) return;
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(part, short(0), KS * (NB * 256) * int(sizeof(float)), 0x00020000);
+    constexpr int kSc1 = 16;  // cache policy bit sc1
+    float V[kWideMaxSplits][kOut];
+#pragma unroll
+    for (int z = 0; z < kWideMaxSplits; ++z)
+#pragma unroll
+      for (int i = 0; i < kOut; ++i) {
+        const int zz = z < KS ? z : KS - 1;  // past the last split: re-read it, not added
+        V[z][i] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(prs, (t + 64 * kWideWaves * i) * 4, zz * NB * 1024, kSc1));
+      }
+#pragma unroll
+    for (int i = 0; i < kOut; ++i) {
+      float x = 0.0f;
+#pragma unroll
+      for (int z = 0; z < kWideMaxSplits; ++z) x = z < KS ? x + V[z][i] : x;
+      v[i] = x;
+    }
+  }
+  if constexpr (RES) {
+    // residual += C; xbf = bf16(residual); the tile's 128 columns' sums of squares per row: this
+    // thread's values (blocks j and j + 2 of row 4 (l / 32) + e), then the 32 lanes of each half
+    // wave, then the two waves of each row in wave order
+    const int e = (t >> 6) & 3, l = t & 63, row = 4 * (l >> 5) + e;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kOut; ++i) {
+      const int j = (t + 64 * kWideWaves * i) >> 8;
+      const int col = tn * (32 * NB) + 32 * j + (l & 31);
+      if (row < a.m) {
+        float* res = a.residual + size_t(row) * a.n + col;
+        const float x = *res + v[i];
+        *res = x;
+        a.xbf[size_t(row) * a.n + col] = bf16_bits(x);
+        ss += x * x;
+      }
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((lane & 31) == 0) sh.ss[wave][lane >> 5] = ss;
+    __syncthreads();
+    if (threadIdx.x < kWideRows) {
+      // row r = 4 h + e: waves e and e + 4 (blocks 0-1 and 2-3 of element e), half h
+      const int r = threadIdx.x, ee = r & 3, h = r >> 2;
+      if (r < a.m) a.partials_out[size_t(r) * a.norm_blocks + tn] = sh.ss[ee][h] + sh.ss[ee + 4][h];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kOut; ++i) {
+      const int x = t + 64 * kWideWaves * i, j = x >> 8, e = (x >> 6) & 3, l = x & 63;
+      const int row = 4 * (l >> 5) + e, col = tn * (32 * NB) + 32 * j + (l & 31);
+      if (row >= a.m || col >= a.n_store) continue;
+      const float y = v[i] * sh.rs[row];
+      if (a.kind == Q38A_EPI_STORE_F32) static_cast<float*>(a.out)[size_t(row) * a.ldo + col] = y;
+      else static_cast<uint16_t*>(a.out)[size_t(row) * a.ldo + col] = bf16_bits(y);
+    }
+  }
+}
+
+// The wide-tile plan of a GEMM, or tiles = 0 when the shape does not take it: decode-size M, a
+// store epilogue on a weight wide enough to fill the CUs with 64-column tiles (no split-K), or the
+// residual epilogue on 128-column tiles with K split to fill the CUs.
+struct WidePlan {
+  int nb, tiles, splits;
+};
+
+WidePlan plan_wide(int m, int n, int k, int kind, int cus) {
+  WidePlan p{0, 0, 1};
+  const int G = k / 64;
+  if (m > kWideRows) return p;
+  if (kind != Q38A_EPI_RESIDUAL) {
+    if (n / 64 >= (3 * cus) / 4 && wide_chunks(2, G) >= kWideWaves) p = WidePlan{2, n / 64, 1};
+  } else if (n % 128 == 0) {
+    const int tiles = n / 128;
+#ifdef WKS
+    int s = WKS;
+#else
+    int s = cus / tiles;
+#endif
+    if (s > kWideMaxSplits) s = kWideMaxSplits;
+    while (s > 1 && wide_chunks(4, G / s) < kWideWaves) --s;
+    if (s >= 1 && tiles * s >= cus / 2 && wide_chunks(4, G / s) >= kWideWaves) p = WidePlan{4, tiles, s};
+  }
+  return p;
 }
 
 // Split-K plan. Small M (qgemv_kernel, one 1024-thread workgroup per CU): slices of at most
@@ -1102,6 +1218,12 @@ int gemm_workspace_size(int m, int n, int k, int cus, size_t out[2]) {
   const size_t tiles = size_t(p.tiles_m) * p.tiles_n;
   out[0] = p.splits > 1 ? tiles * p.splits * size_t(32 * p.mb) * kTileN : 0;
   out[1] = p.splits > 1 ? tiles : 0;
+  // the wide-tile kernel's split partials (residual epilogue), whichever epilogue the caller uses
+  const WidePlan wp = plan_wide(m, n, k, Q38A_EPI_RESIDUAL, cus);
+  if (wp.tiles > 0 && wp.splits > 1) {
+    out[0] = std::max(out[0], size_t(wp.tiles) * wp.splits * wp.nb * 256);
+    out[1] = std::max(out[1], size_t(wp.tiles));
+  }
   return Q38A_OK;
 }
 
@@ -1201,18 +1323,27 @@ int launch_qgemm(const uint16_t* A, int m, const q38a_bq_weight& w, const q38a_g
     if (int rc = check_hip(hipGetLastError(), "qgemm launch")) return rc;
     return mode == 1 ? launch_qk_norm_rope_append(*ap, *b, *kv, stream) : Q38A_OK;
   }
-  // decode-size M with a store epilogue on a wide weight: the 64-column-tile kernel, no split-K. With
-  // the append requested, that GEMM and then the append launch (the same bits as the two calls).
-  const int wide_tiles = w.n / kWideCols;
-  if (m <= kWideRows && mode != 2 && ep.kind != Q38A_EPI_RESIDUAL && wide_tiles >= (3 * cus) / 4 &&
-      wide_chunks(w.k / 64) >= kWideWaves) {
+  // decode-size M on a wide weight: the wide-tile kernel (store epilogues: 64-column tiles, no
+  // split-K; residual: 128-column tiles, K split). With the append requested, that GEMM and then the
+  // append launch (the same bits as the two calls).
+  const WidePlan wp = mode == 2 ? WidePlan{0, 0, 1} : plan_wide(m, w.n, w.k, ep.kind, cus);
+  if (wp.tiles > 0 && (wp.splits == 1 || (ws.partials && ws.counters &&
+                                          ws.partial_floats >= size_t(wp.tiles) * wp.splits * wp.nb * 256 &&
+                                          ws.num_counters >= wp.tiles))) {
     if (mode == 1) g.kind = ep.kind;
+    const dim3 wgrid(unsigned(wp.tiles), unsigned(wp.splits)), wblock(64 * kWideWaves);
+#define Q38A_WIDE(B)                                                                            \
+  case B:                                                                                       \
+    if (wp.nb == 4) hipLaunchKernelGGL((qgemv_wide_kernel<B, 4, true>), wgrid, wblock, 0, stream, g); \
+    else hipLaunchKernelGGL((qgemv_wide_kernel<B, 2, false>), wgrid, wblock, 0, stream, g);       \
+    break;
     switch (w.bits) {
-      case 4: hipLaunchKernelGGL((qgemv_wide_kernel<4>), dim3(unsigned(wide_tiles)), dim3(64 * kWideWaves), 0, stream, g); break;
-      case 5: hipLaunchKernelGGL((qgemv_wide_kernel<5>), dim3(unsigned(wide_tiles)), dim3(64 * kWideWaves), 0, stream, g); break;
-      case 6: hipLaunchKernelGGL((qgemv_wide_kernel<6>), dim3(unsigned(wide_tiles)), dim3(64 * kWideWaves), 0, stream, g); break;
+      Q38A_WIDE(4)
+      Q38A_WIDE(5)
+      Q38A_WIDE(6)
       default: return set_error(Q38A_ERR_UNSUPPORTED, "qgemm: %d-bit weights are not supported", w.bits);
     }
+#undef Q38A_WIDE
     if (int rc = check_hip(hipGetLastError(), "qgemm launch")) return rc;
     return mode == 1 ? launch_qk_norm_rope_append(*ap, *b, *kv, stream) : Q38A_OK;
   }

@@ -335,10 +335,11 @@ def test_in_projection_fused_append_matches_unfused(orc, seqs):
 ])
 @pytest.mark.parametrize("in_loader", [False, True])
 def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n, in_loader):
-    """q38a_qgemm_merge_oproj (the merge kernel then the GEMM) and q38a_qgemm_merge_oproj_in_loader
-    (the merge inside the o-projection's A staging, or for more than 32 rows as the former) equal
-    q38a_attention_decode followed by q38a_qgemm on its out, bit for bit in residual, xbf and
-    partials_out; that GEMM against the oracle's."""
+    """q38a_qgemm_merge_oproj (the merge kernel then the GEMM) equals q38a_attention_decode followed
+    by q38a_qgemm on its out, bit for bit in out, residual, xbf and partials_out, and that GEMM matches
+    the oracle's. q38a_qgemm_merge_oproj_in_loader (the merge inside the split-K kernel's A staging,
+    or for more than 32 rows as the former) matches the oracle at the GEMM tolerance (at <= 8 rows
+    the two-call path's GEMM is the wide-tile kernel, whose sums run in another order)."""
     from gpu_util import attention_params
     from util import randn_bf16
     rng = np.random.default_rng(77)
@@ -380,10 +381,15 @@ def test_merge_oproj_matches_decode_then_gemm(orc, ctxs, n, in_loader):
 
     r_u, x_u, p_u, a_u = run(False)
     r_f, x_f, p_f, a_f = run(True)
-    assert_bits_equal(r_f, r_u, "residual")
-    assert_bits_equal(x_f, x_u, "xbf")
-    assert_bits_equal(p_f, p_u, "partials_out")
-    if B > 32 or not in_loader:  # the merge kernel wrote out
-        assert_bits_equal(a_f, a_u, "out")
     a = a_u.reshape(B, NQ * HD)
+    if in_loader and B <= 32:
+        # the merged A rows are the merge kernel's bits, but the GEMM is the split-K kernel (the
+        # two-call path takes the wide-tile kernel at <= 8 rows, which sums in another order): both
+        # against the oracle
+        check_residual(orc, w, a, res0, r_f.reshape(B, n), x_f.reshape(B, n), p_f.reshape(B, n // 128))
+    else:
+        assert_bits_equal(r_f, r_u, "residual")
+        assert_bits_equal(x_f, x_u, "xbf")
+        assert_bits_equal(p_f, p_u, "partials_out")
+        assert_bits_equal(a_f, a_u, "out")  # the merge kernel wrote out
     check_residual(orc, w, a, res0, r_u.reshape(B, n), x_u.reshape(B, n), p_u.reshape(B, n // 128))
