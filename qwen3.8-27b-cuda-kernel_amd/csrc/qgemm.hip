@@ -1032,10 +1032,15 @@ __global__ void __launch_bounds__(64 * kWideWaves) qgemv_wide_kernel(GemmArgs a)
     u32x4 Ab[1][4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) Ab[0][s] = sh.a[wave][d][2 * s + kg][lane & 7];
-    float16_t S;
+    // S (the rows' sums over the group) from two 16 x 16 x 32 MFMAs against ones: MFMA row r is
+    // A row 4 (r / 8) + r % 4, so that output element e of lane l is row 4 (l / 32) + e, the row of
+    // C element e (rows >= 8 of the 32 x 32 output are never read)
+    float4_t S = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, Ab[0][s]), ones, s == 0 ? float16_t{} : S, 0, 0, 0);
+    for (int h = 0; h < 2; ++h)
+      S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8_t, sh.a[wave][d][4 * h + (lane >> 4)][4 * ((lane >> 3) & 1) + (lane & 3)]), ones, S,
+          0, 0, 0);
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       float16_t T[1];
