@@ -539,12 +539,14 @@ qgemm_kernel(GemmArgs a, AppendArgs ap, BatchArgs batch, KvArgs kv, MergeIn) {
 constexpr int kBigRows = 256;
 constexpr int kBigWaves = 8;
 constexpr int kBigThreads = 64 * kBigWaves;
-constexpr int kBigAStride = 64 + 8;  // bf16 per staged A row (16 B of padding: conflict-free reads)
 
 struct alignas(16) BigShared {
-  uint16_t b[2][8][4][64][8];           // two groups of the tile's weights: [block][step][lane][k]
-  uint16_t a[2][kBigRows][kBigAStride];  // two groups of the tile's A rows
-  float rs[kBigRows];                    // row scales of the folded RMSNorm
+  uint16_t b[2][8][4][64][8];  // two groups of the tile's weights: [block][step][lane][k]
+  // two groups of the tile's A rows, copied by the DMA path of buffer loads (no registers): row r's
+  // 16-byte chunk c (k 8 c .. 8 c + 7) sits in slot c ^ (r % 8), so the MFMA reads of one chunk
+  // over 8 consecutive rows hit 8 different bank groups
+  u32x4 a[2][kBigRows][8];
+  float rs[kBigRows];  // row scales of the folded RMSNorm
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -602,6 +604,18 @@ __device__ inline void load_bwords_lane(BWords& b, const BPlanes& p, int nb, int
   b.scale = __builtin_amdgcn_raw_buffer_load_b16(p.sc, (unit0 * 32 + (l & 31)) * 2, g * 64, 0);
 }
 
+// Step S of dequant_to_lds (the group's k 16 S .. 16 S + 15 of this lane word).
+template <int BITS, int S>
+__device__ inline void dequant_step_to_lds(BigShared& sh, int buf, const BWords& b, int blk, int l) {
+  const float sc = bf16_value(uint16_t(b.scale));
+  const float sneg = -(128.0f + float(1 << (BITS - 1))) * sc;
+  float x[8];
+  step_codes<BITS, S>(b, x);
+  const u32x4 w{scaled_pair(x[0], x[1], sc, sneg), scaled_pair(x[2], x[3], sc, sneg),
+                scaled_pair(x[4], x[5], sc, sneg), scaled_pair(x[6], x[7], sc, sneg)};
+  *reinterpret_cast<u32x4*>(&sh.b[buf][blk][S][l][0]) = w;
+}
+
 template <int BITS>
 __device__ inline void dequant_to_lds(BigShared& sh, int buf, const BWords& b, int blk, int l) {
   const float sc = bf16_value(uint16_t(b.scale));
@@ -641,18 +655,15 @@ qgemm_big_kernel(GemmArgs a) {
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       uniform_ptr(const_cast<uint16_t*>(a.a) + size_t(m0) * a.k), short(0), valid_rows * a.k * int(sizeof(uint16_t)),
       0x00020000);
-  auto load_a = [&](u32x4 (&v)[4], int g) {
+  // A rows of group g into buffer buf by the DMA path: wave w copies rows 32 w .. 32 w + 31 in four
+  // 1 KB instructions (8 rows each; lane l: row 8 i + l / 8, slot l % 8, i.e. chunk (l % 8) ^ (row % 8))
+  auto dma_a = [&](int g, int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = int(threadIdx.x) + i * kBigThreads, r = c >> 3, kc = c & 7;
-      v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ars, (r * a.k + 8 * kc) * 2, 128 * g, 0));
-    }
-  };
-  auto store_a = [&](const u32x4 (&v)[4], int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = int(threadIdx.x) + i * kBigThreads, r = c >> 3, kc = c & 7;
-      *reinterpret_cast<u32x4*>(&sh.a[buf][r][8 * kc]) = v[i];
+      const int r = 32 * wave + 8 * i + (lane >> 3), c = (lane & 7) ^ (r & 7);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ars, (__attribute__((address_space(3))) void*)&sh.a[buf][32 * wave + 8 * i][0], 16, (r * a.k + 8 * c) * 2,
+          128 * g, 0, 0);
     }
   };
 
@@ -663,41 +674,54 @@ qgemm_big_kernel(GemmArgs a) {
     for (int j = 0; j < 4; ++j) C[mb][j] = float16_t{};
 
   if (threadIdx.x < kBigRows) sh.rs[threadIdx.x] = row_scale(a, m0 + threadIdx.x);
-  {
-    BWords b0;
-    u32x4 a0[4];
-    load_bwords_lane<BITS>(b0, bp, dnb, 0, G, dl);
-    load_a(a0, 0);
-    dequant_to_lds<BITS>(sh, 0, b0, dblk, dl);
-    store_a(a0, 0);
-  }
-  __syncthreads();
   const int glast = G - 1;
-  for (int g = 0; g < G; ++g) {
-    const int cur = g & 1;
-    // the next group's weights and A rows in flight while this group's MFMAs run
-    const int gn = g + 1 < glast ? g + 1 : glast;
-    BWords bn;
-    u32x4 an[4];
-    load_bwords_lane<BITS>(bn, bp, dnb, gn, G, dl);
-    load_a(an, gn);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
+  auto gcl = [&](int g) { return g < glast ? g : glast; };
+  // the weights two groups ahead in registers: bq[g & 1] holds group g until its dequantisation
+  BWords bq[2];
+  dma_a(0, 0);
+  load_bwords_lane<BITS>(bq[0], bp, dnb, 0, G, dl);
+  load_bwords_lane<BITS>(bq[1], bp, dnb, gcl(1), G, dl);
+  dequant_to_lds<BITS>(sh, 0, bq[0], dblk, dl);
+  __builtin_amdgcn_s_waitcnt(0);  // the DMA copies of group 0 have landed
+  __syncthreads();
+  // one group: cur = g & 1 (a compile-time constant, so the register ring is indexed statically)
+  auto group = [&](int g, auto curc) {
+    constexpr int cur = decltype(curc)::value;
+    // the next group's A rows into the other buffer (read during the previous group, before its
+    // barrier), then group g + 2's weights into the registers group g held
+    dma_a(gcl(g + 1), cur ^ 1);
+    load_bwords_lane<BITS>(bq[cur], bp, dnb, gcl(g + 2), G, dl);
+    const BWords& bnext = bq[cur ^ 1];
+    auto step = [&](auto st) {
+      constexpr int s = decltype(st)::value;
       bf16x8_t ao[2];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-        ao[mb] = *reinterpret_cast<const bf16x8_t*>(&sh.a[cur][64 * wm + 32 * mb + (lane & 31)][16 * s + 8 * kg]);
+      for (int mb = 0; mb < 2; ++mb) {
+        const int r = 64 * wm + 32 * mb + (lane & 31);
+        ao[mb] = __builtin_bit_cast(bf16x8_t, sh.a[cur][r][(2 * s + kg) ^ (r & 7)]);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bf16x8_t bo = *reinterpret_cast<const bf16x8_t*>(&sh.b[cur][4 * wn + j][s][lane][0]);
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) C[mb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao[mb], bo, C[mb][j], 0, 0, 0);
       }
-    }
-    // (past the last group: a copy nobody reads)
-    dequant_to_lds<BITS>(sh, cur ^ 1, bn, dblk, dl);
-    store_a(an, cur ^ 1);
+      // group g + 1's step s dequantised into the other buffer while these MFMAs run (past the last
+      // group: a copy nobody reads)
+      dequant_step_to_lds<BITS, s>(sh, cur ^ 1, bnext, dblk, dl);
+    };
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
+    // the DMA copies of group g + 1 have landed (the weight loads issued after them may still be
+    // in flight: vmcnt counts in order, three loads per lane word, two for 4-bit weights)
+    __builtin_amdgcn_s_waitcnt(BITS == 4 ? 0x0F72 : 0x0F73);
     __syncthreads();
+  };
+  for (int g = 0; g < G; g += 2) {
+    group(g, std::integral_constant<int, 0>{});
+    if (g + 1 < G) group(g + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- epilogue: C element e of (mb, j): row 64 wm + 32 mb + 8 (e / 4) + 4 kg + e % 4, column
