@@ -42,42 +42,6 @@ __device__ inline int exponent_of_f64(double x) {
   return int((__builtin_bit_cast(uint64_t, x) >> 52) & 0x7ff) - 1023;
 }
 
-// Cross-lane exchanges on the VALU (DPP and permlane swaps) instead of LDS-routed shuffles: the
-// norm's reductions are a dependent chain, and each ds_bpermute step costs an LDS round trip.
-// dpp_move<C>(x): lane i receives x of the lane that DPP control C names (all lanes valid here).
-template <int C>
-__device__ inline uint32_t dpp_move(uint32_t x) {
-  return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), C, 0xf, 0xf, false));
-}
-constexpr int kDppXor1 = 0xb1;        // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4e;        // quad_perm [2, 3, 0, 1]
-constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within each 8
-constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within each 16
-constexpr int kDppRor8 = 0x128;       // lane i <- (i + 8) mod 16 within each 16 (= i ^ 8)
-constexpr int kDppRor4 = 0x124;       // lane i <- (i + 4) mod 16 within each 16
-
-// op over all 64 lanes, the result in every lane (op commutative and associative). After the
-// quad steps a quad holds its total; the mirrors pair quad 0 with quad 1 and the two halves of a
-// 16-lane row; the swaps pair rows 0-1 / 2-3, then the two halves of the wave.
-template <class Op>
-__device__ inline uint32_t wave_allreduce(uint32_t x, Op op) {
-  x = op(x, dpp_move<kDppXor1>(x));
-  x = op(x, dpp_move<kDppXor2>(x));
-  x = op(x, dpp_move<kDppHalfMirror>(x));
-  x = op(x, dpp_move<kDppMirror>(x));
-  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-  x = op(a[0], a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-  return op(b[0], b[1]);
-}
-
-__device__ inline int wave_min_i32(int x) {
-  return int(wave_allreduce(uint32_t(x), [](uint32_t a, uint32_t b) { return uint32_t(min(int(a), int(b))); }));
-}
-__device__ inline int wave_max_i32(int x) {
-  return int(wave_allreduce(uint32_t(x), [](uint32_t a, uint32_t b) { return uint32_t(max(int(a), int(b))); }));
-}
-
 // Sum over the wave in double, in a fixed tree order (the callers use it only where every order
 // gives the same, exact, sum).
 __device__ inline double wave_sum(double v) {

@@ -112,6 +112,70 @@ __device__ inline float fast_sigmoid(float g) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504088896341f * g));
 }
 
+// ---- cross-lane steps on the VALU ----------------------------------------------------------------
+// DPP moves and permlane swaps instead of LDS-routed shuffles (__shfl*: one ds_bpermute, an LDS
+// round trip, per step of a dependent chain). Every lane of the wave must be active.
+// dpp_move<C>(x): lane i receives x of the lane that DPP control C names (all lanes valid here).
+template <int C>
+__device__ inline uint32_t dpp_move(uint32_t x) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), C, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xb1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4e;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within each 8
+constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within each 16
+constexpr int kDppRor8 = 0x128;       // lane i <- (i + 8) mod 16 within each 16 (= i ^ 8)
+constexpr int kDppRor4 = 0x124;       // lane i <- (i + 4) mod 16 within each 16
+
+// op over all 64 lanes, the result in every lane (op commutative and associative). After the
+// quad steps a quad holds its total; the mirrors pair quad 0 with quad 1 and the two halves of a
+// 16-lane row; the swaps pair rows 0-1 / 2-3, then the two halves of the wave.
+template <class Op>
+__device__ inline uint32_t wave_allreduce(uint32_t x, Op op) {
+  x = op(x, dpp_move<kDppXor1>(x));
+  x = op(x, dpp_move<kDppXor2>(x));
+  x = op(x, dpp_move<kDppHalfMirror>(x));
+  x = op(x, dpp_move<kDppMirror>(x));
+  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = op(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return op(b[0], b[1]);
+}
+
+__device__ inline int wave_min_i32(int x) {
+  return int(wave_allreduce(uint32_t(x), [](uint32_t a, uint32_t b) { return uint32_t(min(int(a), int(b))); }));
+}
+__device__ inline int wave_max_i32(int x) {
+  return int(wave_allreduce(uint32_t(x), [](uint32_t a, uint32_t b) { return uint32_t(max(int(a), int(b))); }));
+}
+
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele within each 16-lane row (row_shr 1, 2, 4,
+// 8, zeros shifted in), then row 0's total into row 1 and row 2's into row 3 (row_bcast15), then
+// lane 31's running total into rows 2 and 3 (row_bcast31).
+__device__ inline int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
+  return x;
+}
+
+// x op (x of lane l ^ 32) in every lane l
+__device__ inline float xor32_max(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ inline float xor32_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ inline float xor16_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+
 // ---- MFMA operand types (gfx950) ----------------------------------------------------------------
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));

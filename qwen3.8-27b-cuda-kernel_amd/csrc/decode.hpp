@@ -589,8 +589,8 @@ __device__ void finish_item(const DecodeArgs& a, WaveMerge<W>& sm, int b, int kv
                             const float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = a.group;
-  l_run += __shfl_xor(l_run, 16, 64);  // l over the 4 quads of each head lane
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = xor16_sum(l_run);  // l over the 4 quads of each head lane
+  l_run = xor32_sum(l_run);
   if (lane < G) {
     sm.m[wave][lane] = m_run;
     sm.l[wave][lane] = l_run;

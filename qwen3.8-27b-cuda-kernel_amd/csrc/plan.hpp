@@ -96,15 +96,9 @@ __device__ inline void block_scan_store(const int (&v)[kPlanPer], int B, int* ds
 // Decode plan, computed by every wave on its own (no LDS, no barrier), so a workgroup's first loads
 // wait only for the sequence metadata. Sequences are scanned 64 at a time, one per lane.
 __device__ inline int wave_sum_i(int x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
+  return int(wave_allreduce(uint32_t(x), [](uint32_t a, uint32_t b) { return a + b; }));
 }
-__device__ inline int wave_max_i(int x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = max(x, __shfl_xor(x, off, 64));
-  return x;
-}
+__device__ inline int wave_max_i(int x) { return wave_max_i32(x); }
 
 struct DecodePlan {
   int cp;      // pages per item (wave-uniform)
@@ -153,20 +147,15 @@ __device__ inline ItemSpot wave_locate(const BatchArgs& batch, int nkv, const De
   for (int s0 = 0; s0 < batch.num_seqs && base <= item; s0 += 64) {
     const int p = s0 == 0 ? pl.pages0 : decode_pages(batch, s0 + lane);
     const int n = ceil_div_i(p, pl.cp) * nkv;
-    int incl = n;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int x = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += x;
-    }
+    const int incl = wave_incl_scan(n);
     const int excl = base + incl - n;
     const unsigned long long hit = __ballot(n > 0 && excl <= item && item < excl + n);
     if (hit) {
       const int l = __builtin_ctzll(hit);
       r.seq = s0 + l;
-      r.local = item - __shfl(excl, l, 64);
+      r.local = item - __builtin_amdgcn_readlane(excl, l);
     }
-    base += __shfl(incl, 63, 64);
+    base += __builtin_amdgcn_readlane(incl, 63);
   }
   r.seq = __builtin_amdgcn_readfirstlane(r.seq);
   r.local = __builtin_amdgcn_readfirstlane(r.local);

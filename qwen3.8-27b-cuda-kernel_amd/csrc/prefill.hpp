@@ -475,7 +475,7 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
 #pragma unroll
     for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, S[e]);
     // scores enter the exp2 domain as S * kScoreScale (> 0, so the max commutes with it)
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * kScoreScale;
+    tmax = xor32_max(tmax) * kScoreScale;
     // Lazy rescaling: the running reference max only moves when a tile's max exceeds it by more
     // than kRescaleSlack (log2 units), so probabilities stay below 2^kRescaleSlack (exact enough in
     // fp16 and fp32) and the O rescale is almost never needed after the first tiles.
@@ -549,7 +549,7 @@ __device__ __attribute__((always_inline)) inline void prefill_unit(const Prefill
     __syncthreads();
   }
 
-  const float lt = l_run + __shfl_xor(l_run, 32, 64);
+  const float lt = xor32_sum(l_run);
   if (!row_ok) return;
   if (parts > 1) {  // partial row (kPartialRowFloats): O / l as fp16 [256], then m, l (fp32)
     float* row = partial + size_t(my_row - r0) * kPartialRowFloats;
