@@ -666,11 +666,13 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
     const ItemSpot at = wave_locate(batch, a.nkv, pl, item);
     if (at.seq < 0) break;
     const int b = at.seq;
+    // the row's block-table row is read beside its length, in the same round trip
+    const int slot = batch.seq_slot[b];
     const int L = decode_len(batch, b);
     const int nsplit = ceil_div_i(ceil_div_i(L, kPageTokens), cp);
     const int kvh = at.local / nsplit, split = at.local % nsplit;
     const int span = cp * kPageTokens;  // tokens per split
-    const int* bt = kv.block_table + size_t(batch.seq_slot[b]) * kv.max_pages_per_seq;
+    const int* bt = kv.block_table + size_t(slot) * kv.max_pages_per_seq;
     const int q_row = batch.seq_start[b];
     float m_run = -INFINITY, l_run = 0.f;
     float4_t O[16];
