@@ -374,7 +374,9 @@ struct BlockSource {
 // computed, and with a claim counter the claim after that is in flight too. Block indices, pages
 // and block-table reads are wave-uniform; blocks past te are masked. The waves of a workgroup do
 // not synchronise here: each loads its q operand straight from global memory.
-template <bool VT>
+// kQBuf: q through a bounds-checked buffer load (no select on its values); the ragged launch keeps
+// the select form, which measured faster there.
+template <bool VT, bool kQBuf = false>
 __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const int* bt, int kvh, int q_row,
                                  const BlockSource& src, float& m_run, float& l_run, float4_t (&O)[16]) {
   const int lane = threadIdx.x & 63;
@@ -385,15 +387,30 @@ __device__ void decode_item_int8(const DecodeArgs& a, const KvArgs& kv, const in
   // does not wait for them.
   half8_t qf[4][2];
   {
-    const bool real = n16 < a.group;
-    const uint16_t* qlane = a.q + (size_t(q_row) * a.nq + kvh * a.group + (real ? n16 : 0)) * kHeadDim + 16 * j4;
+    if constexpr (kQBuf) {
+      // a buffer over the group's q rows: lanes of rows past the group read past its end and get
+      // zeros from the bounds check, so no select on the loaded values makes anything wait for q
+      // before the first K/V loads go out
+      const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(a.q + (size_t(q_row) * a.nq + kvh * a.group) * kHeadDim), short(0),
+          a.group * kHeadDim * 2, 0x00020000);
+      const int qoff = n16 < a.group ? n16 * kHeadDim * 2 + 32 * j4 : 0x7ffffff0;
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        half8_t x = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
-        qf[g][h] = real ? x : half8_t{};
-      }
+        for (int h = 0; h < 2; ++h)
+          qf[g][h] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(qr, qoff, 128 * g + 16 * h, 0));
+    } else {
+      const bool real = n16 < a.group;
+      const uint16_t* qlane = a.q + (size_t(q_row) * a.nq + kvh * a.group + (real ? n16 : 0)) * kHeadDim + 16 * j4;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          half8_t x = *reinterpret_cast<const half8_t*>(qlane + 64 * g + 8 * h);
+          qf[g][h] = real ? x : half8_t{};
+        }
+    }
   }
   const uint8_t* layer = kv.pool + size_t(a.attn_layer) * kv.layer_stride;
   const Int8Offsets off = int8_offsets<VT>(kv.layout, kvh, n16, j4);
@@ -666,14 +683,24 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
     const ItemSpot at = wave_locate(batch, a.nkv, pl, item);
     if (at.seq < 0) break;
     const int b = at.seq;
-    // the row's block-table row is read beside its length, in the same round trip
-    const int slot = batch.seq_slot[b];
-    const int L = decode_len(batch, b);
+    // the row's metadata and block-table slot in one round trip: scalar loads in the decode launch
+    // (through the constant address space; the launch metadata is read-only), vector loads in the
+    // ragged launch (where the scalar form measured 2% slower on config 4)
+    int slot, q_row, q_end, pos0;
+    if constexpr (W == kWaves) {
+      scalar_load4(batch.seq_slot, b, batch.seq_start, b, batch.seq_start, b + 1, batch.seq_pos0, b, slot, q_row, q_end,
+                   pos0);
+    } else {
+      slot = batch.seq_slot[b];
+      q_row = batch.seq_start[b];
+      q_end = batch.seq_start[b + 1];
+      pos0 = batch.seq_pos0[b];
+    }
+    const int L = q_end - q_row == 1 ? pos0 + 1 : 0;
     const int nsplit = ceil_div_i(ceil_div_i(L, kPageTokens), cp);
     const int kvh = at.local / nsplit, split = at.local % nsplit;
     const int span = cp * kPageTokens;  // tokens per split
     const int* bt = kv.block_table + size_t(slot) * kv.max_pages_per_seq;
-    const int q_row = batch.seq_start[b];
     float m_run = -INFINITY, l_run = 0.f;
     float4_t O[16];
 #pragma unroll
@@ -697,7 +724,7 @@ __device__ __attribute__((always_inline)) inline void decode_items(const DecodeA
       }
       src.nblk = ceil_div_i(src.te - src.tb, 16);
       src.stride = W;
-      decode_item_int8<DT == Q38A_KV_INT8_VT>(a, kv, bt, kvh, q_row, src, m_run, l_run, O);
+      decode_item_int8<DT == Q38A_KV_INT8_VT, W == kWaves>(a, kv, bt, kvh, q_row, src, m_run, l_run, O);
     } else {
       const int t_begin = split * span;
       decode_item_bf16<W>(a, kv, bt, kvh, q_row, t_begin, min(L, t_begin + span), m_run, l_run, O);

@@ -29,6 +29,23 @@ struct PlanShared {
 };
 
 // Keys of decode row b (a sequence with exactly one token in the step): [0, seq_pos0[b] + 1).
+// p[i] for a wave-uniform i as a scalar load (through the constant address space: only for data no
+// kernel of the launch writes)
+__device__ inline int scalar_load(const int* p, int i) {
+  return reinterpret_cast<const __attribute__((address_space(4))) int*>(reinterpret_cast<uintptr_t>(p))[i];
+}
+
+// Four such loads issued together (the compiler otherwise sinks a load to its first use, behind
+// the others' round trip).
+__device__ inline void scalar_load4(const int* p0, int i0, const int* p1, int i1, const int* p2, int i2, const int* p3,
+                                    int i3, int& v0, int& v1, int& v2, int& v3) {
+  typedef const volatile __attribute__((address_space(4))) int* cp;
+  v0 = reinterpret_cast<cp>(reinterpret_cast<uintptr_t>(p0))[i0];
+  v1 = reinterpret_cast<cp>(reinterpret_cast<uintptr_t>(p1))[i1];
+  v2 = reinterpret_cast<cp>(reinterpret_cast<uintptr_t>(p2))[i2];
+  v3 = reinterpret_cast<cp>(reinterpret_cast<uintptr_t>(p3))[i3];
+}
+
 __device__ inline int decode_len(const BatchArgs& b, int s) {
   // the three loads are independent (seq_pos0 is read whatever the row's length), so they are one
   // round trip to memory rather than two
