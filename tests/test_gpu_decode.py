@@ -144,3 +144,16 @@ def test_decode_config1_golden():
     assert_bits_equal(pool.download(), expected_pool(g), "pool bytes")
     check_close(bf16_bits_to_f32(host(out_t, np.uint16))[None], bf16_bits_to_f32(g["out_bf16"])[None],
                 what="config 1 output vs reference")
+
+
+@pytest.mark.parametrize("B", [65, 200])
+def test_decode_more_than_64_rows(orc, B):
+    """More decode rows than a wave has lanes: the plan's per-64-row passes (page sums, the item
+    scan and its running base across passes) and items of rows past 64; some rows are empty-prefix
+    (context 0) and some long."""
+    rng = np.random.default_rng(40 + B)
+    ctxs = [int(x) for x in rng.integers(0, 400, B)]
+    ctxs[3] = 0
+    ctxs[B - 1] = 3000
+    ctxs[70 % B] = 1500
+    decode_step(orc, ctxs, q38a.KV_INT8, seed=41 + B, max_splits=32)

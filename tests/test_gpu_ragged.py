@@ -133,3 +133,11 @@ def test_ragged_back_to_back_launches(orc):
     decode = [(c, 1) for c in (4000, 129, 20000, 640)]
     for i, seqs in enumerate([mixed, decode, mixed, decode, [(6000, 300)], mixed]):
         ragged_step(orc, seqs, seed=40 + i)
+
+
+def test_ragged_more_than_64_decode_rows(orc):
+    """A chunk beside 100 decode rows: the decode items of rows past 64 in the ragged launch."""
+    rng = np.random.default_rng(50)
+    seqs = [(int(x), 1) for x in rng.integers(0, 600, 100)]
+    seqs[10] = (700, 40)
+    ragged_step(orc, seqs, seed=51)
