@@ -405,10 +405,21 @@ def runner_decode_config(steps, warmup, layers=16, ctxs=None, name="decode_b8_16
         e.record()
         torch.cuda.synchronize()
         out[mode] = a.elapsed_time(e) / steps
+        # host time to issue one step (the previous step has finished, so nothing waits): what the
+        # calling thread spends per step, free for scheduling while the GPU runs the step
+        t_issue = 0.0
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            r.decode(rows, s)
+            t_issue += time.perf_counter() - t0
+        torch.cuda.synchronize()
+        out[mode + "_issue"] = t_issue / steps * 1e6
     kv = layers * sum(c + 1 for c in ctxs) * INT8_TOKEN_BYTES
     r.close()
     return {"config": name, "ctxs": ctxs, "layers": layers, "graph_ms": round(out["graph"], 5),
-            "eager_ms": round(out["eager"], 5), "kv_bytes": kv,
+            "eager_ms": round(out["eager"], 5), "graph_host_issue_us": round(out["graph_issue"], 1),
+            "eager_host_issue_us": round(out["eager_issue"], 1), "kv_bytes": kv,
             "graph_kv_gbs": round(kv / (out["graph"] * 1e-3) / 1e9, 1),
             "graph_tokens_per_s": round(len(ctxs) / (out["graph"] * 1e-3), 1)}
 
