@@ -73,29 +73,16 @@ __host__ __device__ inline float as_f32(uint32_t u) {
   return f;
 }
 
-// IEEE binary16 from binary32, round to nearest even; NaN -> quiet NaN, overflow -> inf.
+// IEEE binary16 from binary32, round to nearest even (subnormals kept, |f| >= 65520 -> inf): the
+// hardware conversion (v_cvt_f16_f32 in the default round-to-nearest-even mode with fp16
+// denormals enabled); NaN -> the canonical quiet NaN with f's sign.
 __device__ inline uint16_t f16_bits(float f) {
-  const uint32_t u = as_u32(f);
-  const uint32_t sign = (u >> 16) & 0x8000u;
-  const uint32_t mag = u & 0x7fffffffu;
-  if (mag > 0x7f800000u) return uint16_t(sign | 0x7e00u);
-  if (mag >= 0x477ff000u) return uint16_t(sign | 0x7c00u);  // |f| >= 65520 rounds to inf
-  if (mag < 0x38800000u) {  // below 2^-14: result is a multiple of 2^-24
-    return uint16_t(sign | uint32_t(__builtin_rintf(as_f32(mag) * 16777216.0f)));
-  }
-  // normal: drop 13 mantissa bits with round-half-even, rebias the exponent 127 -> 15
-  const uint32_t rounded = (mag + 0x0fffu + ((mag >> 13) & 1u)) >> 13;
-  return uint16_t(sign | (rounded - (112u << 10)));
+  const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  return f != f ? uint16_t(((as_u32(f) >> 16) & 0x8000u) | 0x7e00u) : h;
 }
 
-__device__ inline float f16_value(uint16_t h) {
-  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
-  float v;
-  if (e == 0) v = float(m) * 5.9604644775390625e-08f;  // m * 2^-24, exact
-  else if (e == 31) v = as_f32(0x7f800000u | (m << 13));
-  else v = as_f32(((e + 112u) << 23) | (m << 13));
-  return (h & 0x8000u) ? -v : v;
-}
+// binary16 -> binary32, exact (v_cvt_f32_f16).
+__device__ inline float f16_value(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 
 // bfloat16 from binary32, round to nearest even; NaN -> quiet NaN.
 __host__ __device__ inline uint16_t bf16_bits(float f) {
