@@ -15,10 +15,9 @@
 // from a host-built table (same libm calls as the CPU reference), read per position.
 //
 // Sum of squares: the reference sums x_i^2 in double, left to right. x is bf16, so every x_i^2 is
-// exact in double; the sum is exact in any order whenever the nonzero magnitudes span at most 14
-// binades (24 + 2 * 14 <= 53 bits), or whenever the total and the lowest set bit of the squares fit
-// in 53 bits. The kernel checks both (wave reductions) and then uses a tree reduction; otherwise
-// one lane replays the left-to-right double sum from LDS.
+// exact in double; the sum is exact in any order whenever the total and the lowest set bit of the
+// squares fit in 53 bits. The kernel checks that (a wave reduction) and then uses a tree reduction;
+// otherwise one lane replays the left-to-right double sum from LDS.
 #include "append.hpp"
 
 // (append.hpp turns multiply-add contraction off for the whole file.)
